@@ -1,0 +1,302 @@
+// extern "C" entry points declared in include/st_attn.h: argument checks,
+// error reporting and dispatch to the kernel launchers. Nothing here
+// allocates, frees or synchronises.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "../../include/st_attn.h"
+#include "dense.h"
+#include "sparse.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return ST_OK;
+}
+
+int launched(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(ST_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+bool pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+
+int log2i(int64_t x) {
+  int r = 0;
+  while ((int64_t(1) << r) < x) ++r;
+  return r;
+}
+
+int check_dtype(int dtype) {
+  if (dtype != ST_DTYPE_F32 && dtype != ST_DTYPE_F16 && dtype != ST_DTYPE_BF16)
+    return fail(ST_EINVAL, "unknown dtype code %d", dtype);
+  return ST_OK;
+}
+
+int check_envelope(int64_t head_dim, int64_t block_size) {
+  if (!pow2(block_size) || block_size < 2 || block_size > 128)
+    return fail(ST_EUNSUPPORTED, "block_size %lld: the fused kernels need a power of two in [2, 128]",
+                (long long)block_size);
+  if (head_dim > 256 || head_dim % 8 != 0)
+    return fail(ST_EUNSUPPORTED, "head_dim %lld: the fused kernels need head_dim <= 256 and a multiple of 8",
+                (long long)head_dim);
+  return ST_OK;
+}
+
+int check_sizes(int64_t batch, int64_t queries, int64_t keys, int64_t heads, int64_t head_dim,
+                int64_t block_size) {
+  if (batch < 1 || queries < 1 || keys < 1 || heads < 1 || head_dim < 1 || block_size < 1)
+    return fail(ST_EINVAL, "attention dimensions and tile sizes must be positive");
+  if (queries > (int64_t(1) << 30) || keys > (int64_t(1) << 30))
+    return fail(ST_EUNSUPPORTED, "queries and keys must be below 2^30");
+  if (batch * heads > 65535) return fail(ST_EUNSUPPORTED, "batch*heads must be at most 65535");
+  return ST_OK;
+}
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+}  // namespace
+
+extern "C" {
+
+int st_abi_version(void) { return ST_ABI_VERSION; }
+
+const char* st_last_error(void) { return g_last_error.c_str(); }
+
+int st_dense_supported(int dtype, int64_t head_dim, int64_t block_size) {
+  if (check_dtype(dtype) != ST_OK) return 0;
+  return check_envelope(head_dim, block_size) == ST_OK ? 1 : 0;
+}
+
+int st_dense_fwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_t heads,
+                 int64_t head_dim, int64_t block_size, const void* q, const void* k,
+                 const void* v, const int64_t* positions, void* out, float* rc, float* pr,
+                 float* zr, float* z, void* stream) {
+  int e;
+  if ((e = check_dtype(dtype)) || (e = check_sizes(batch, queries, keys, heads, head_dim, block_size)) ||
+      (e = check_envelope(head_dim, block_size)))
+    return e;
+  if (!q || !k || !v || !positions || !out || !rc || !pr || !zr || !z)
+    return fail(ST_EINVAL, "st_dense_fwd: null pointer argument");
+  st::DenseArgs a = {};
+  a.q = q; a.k = k; a.v = v; a.pos = positions;
+  a.out = out; a.rc = rc; a.pr = pr; a.zr = zr; a.z = z;
+  a.B = (int)batch; a.Q = (int)queries; a.N = (int)keys; a.H = (int)heads; a.D = (int)head_dim;
+  a.block = (int)block_size; a.logb = log2i(block_size);
+  a.scale = 1.f / sqrtf((float)head_dim);
+  a.scale_log2 = a.scale * 1.4426950408889634f;
+  return launched(st::launch_dense_fwd(dtype, a, as_stream(stream)), "st_dense_fwd");
+}
+
+size_t st_dense_bwd_workspace_bytes(int64_t batch, int64_t queries, int64_t heads) {
+  return 2 * align256(sizeof(float) * (size_t)batch * queries * heads);
+}
+
+int st_dense_bwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_t heads,
+                 int64_t head_dim, int64_t block_size, const void* q, const void* k,
+                 const void* v, const int64_t* positions, const void* out, const float* rc,
+                 const float* pr, const float* zr, const float* z, const void* dout, void* dq,
+                 void* dk, void* dv, void* workspace, size_t workspace_bytes, void* stream) {
+  int e;
+  if ((e = check_dtype(dtype)) || (e = check_sizes(batch, queries, keys, heads, head_dim, block_size)) ||
+      (e = check_envelope(head_dim, block_size)))
+    return e;
+  if (!q || !k || !v || !positions || !out || !rc || !pr || !zr || !z || !dout || !dq || !dk || !dv ||
+      !workspace)
+    return fail(ST_EINVAL, "st_dense_bwd: null pointer argument");
+  const size_t need = st_dense_bwd_workspace_bytes(batch, queries, heads);
+  if (workspace_bytes < need)
+    return fail(ST_EINVAL, "st_dense_bwd: workspace of %zu bytes, %zu needed", workspace_bytes, need);
+  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+    return fail(ST_EINVAL, "st_dense_bwd: workspace must be 256-byte aligned");
+  st::DenseArgs a = {};
+  a.q = q; a.k = k; a.v = v; a.pos = positions; a.dout = dout;
+  a.out = const_cast<void*>(out);
+  a.rc = const_cast<float*>(rc); a.pr = const_cast<float*>(pr);
+  a.zr = const_cast<float*>(zr); a.z = const_cast<float*>(z);
+  a.delta = reinterpret_cast<float*>(workspace);
+  a.rho = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + need / 2);
+  a.dq = dq; a.dk = dk; a.dv = dv;
+  a.B = (int)batch; a.Q = (int)queries; a.N = (int)keys; a.H = (int)heads; a.D = (int)head_dim;
+  a.block = (int)block_size; a.logb = log2i(block_size);
+  a.scale = 1.f / sqrtf((float)head_dim);
+  a.scale_log2 = a.scale * 1.4426950408889634f;
+  return launched(st::launch_dense_bwd(dtype, a, as_stream(stream)), "st_dense_bwd");
+}
+
+// ---------------------------------------------------------------------------
+// sparse
+
+static int check_kv(const char* who, int64_t block_size, const void* k, const int32_t* page_table,
+                    int64_t page_tokens, int64_t pages_per_seq, int64_t n_tokens, int64_t token_offset) {
+  if (!k) return fail(ST_EINVAL, "%s: null key pointer", who);
+  if (n_tokens < 1 || n_tokens > (int64_t(1) << 40))
+    return fail(ST_EINVAL, "%s: n_tokens must be positive", who);
+  if (token_offset < 0 || token_offset % block_size != 0)
+    return fail(ST_EINVAL, "%s: cache pages/offset must be block aligned", who);
+  if (page_table) {
+    if (page_tokens < block_size || page_tokens % block_size != 0)
+      return fail(ST_EINVAL, "%s: cache pages/offset must be block aligned", who);
+    if (pages_per_seq * page_tokens < n_tokens)
+      return fail(ST_EINVAL, "%s: page table covers %lld tokens, %lld needed", who,
+                  (long long)(pages_per_seq * page_tokens), (long long)n_tokens);
+  }
+  return ST_OK;
+}
+
+static void fill_sparse(st::SparseArgs& a, int64_t batch, int64_t queries, int64_t heads,
+                        int64_t head_dim, int64_t block_size, const void* q, const int64_t* positions,
+                        const void* k, const void* v, const int32_t* page_table, int64_t page_tokens,
+                        int64_t pages_per_seq, int64_t n_tokens, int64_t token_offset) {
+  a = st::SparseArgs{};
+  a.q = q; a.pos = positions;
+  a.kv.k = k; a.kv.v = v; a.kv.page_table = page_table; a.kv.page_tokens = page_tokens;
+  a.kv.pages_per_seq = pages_per_seq; a.kv.n_tokens = n_tokens; a.kv.token_offset = token_offset;
+  a.B = (int)batch; a.Q = (int)queries; a.H = (int)heads; a.D = (int)head_dim;
+  a.block = (int)block_size; a.logb = log2i(block_size);
+  a.n_blocks = (n_tokens + block_size - 1) / block_size;
+  a.id_base = token_offset / block_size;
+  a.scale_log2 = 1.4426950408889634f / sqrtf((float)head_dim);
+}
+
+int st_sparse_scores(int dtype, int64_t batch, int64_t queries, int64_t heads, int64_t head_dim,
+                     int64_t block_size, const void* q, const int64_t* positions, const void* k,
+                     const int32_t* page_table, int64_t page_tokens, int64_t pages_per_seq,
+                     int64_t n_tokens, int64_t token_offset, float* scores, int64_t n_blocks,
+                     void* stream) {
+  int e;
+  if ((e = check_dtype(dtype)) || (e = check_sizes(batch, queries, 1, heads, head_dim, block_size)) ||
+      (e = check_envelope(head_dim, block_size)) ||
+      (e = check_kv("st_sparse_scores", block_size, k, page_table, page_tokens, pages_per_seq, n_tokens,
+                    token_offset)))
+    return e;
+  if (!q || !positions || !scores) return fail(ST_EINVAL, "st_sparse_scores: null pointer argument");
+  st::SparseArgs a;
+  fill_sparse(a, batch, queries, heads, head_dim, block_size, q, positions, k, nullptr, page_table,
+              page_tokens, pages_per_seq, n_tokens, token_offset);
+  if (n_blocks != a.n_blocks)
+    return fail(ST_EINVAL, "st_sparse_scores: n_blocks %lld, the KV range holds %lld", (long long)n_blocks,
+                (long long)a.n_blocks);
+  a.scores = scores;
+  return launched(st::launch_sparse_scores(dtype, a, as_stream(stream)), "st_sparse_scores");
+}
+
+int st_sparse_select(int64_t rows, int64_t n_blocks, int64_t topk, int64_t id_base, const float* scores,
+                     int64_t* ids, float* top_scores, float* log_zr, void* stream) {
+  if (rows < 1 || n_blocks < 1) return fail(ST_EINVAL, "st_sparse_select: rows and n_blocks must be positive");
+  if (topk < 1) return fail(ST_EINVAL, "topk positive; cache pages/offset must be block aligned");
+  if (topk > 4096) return fail(ST_EUNSUPPORTED, "st_sparse_select: topk above 4096");
+  if (n_blocks >= (int64_t(1) << 31)) return fail(ST_EUNSUPPORTED, "st_sparse_select: too many blocks");
+  if (!scores || !ids || !top_scores || !log_zr) return fail(ST_EINVAL, "st_sparse_select: null pointer");
+  return launched(st::launch_sparse_select(rows, n_blocks, (int)topk, id_base, scores, ids, top_scores,
+                                           log_zr, as_stream(stream)),
+                  "st_sparse_select");
+}
+
+size_t st_sparse_workspace_bytes(int64_t batch, int64_t queries, int64_t heads, int64_t head_dim,
+                                 int64_t topk, int64_t n_blocks) {
+  const size_t rows = (size_t)batch * queries * heads;
+  const size_t scores = align256(sizeof(float) * rows * (size_t)n_blocks);
+  const size_t partial =
+      align256(sizeof(float) * rows * (size_t)st::sparse_chunks((int)topk) * (st::sparse_dp((int)head_dim) + 2));
+  return scores + partial;
+}
+
+int st_sparse_pop(int dtype, int64_t batch, int64_t queries, int64_t heads, int64_t head_dim,
+                  int64_t block_size, const void* q, const int64_t* positions, const void* k,
+                  const void* v, const int32_t* page_table, int64_t page_tokens,
+                  int64_t pages_per_seq, int64_t n_tokens, int64_t token_offset,
+                  const int64_t* ids, const float* top_scores, const float* log_zr, int64_t topk,
+                  void* out, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  int e;
+  if ((e = check_dtype(dtype)) || (e = check_sizes(batch, queries, 1, heads, head_dim, block_size)) ||
+      (e = check_envelope(head_dim, block_size)) ||
+      (e = check_kv("st_sparse_pop", block_size, k, page_table, page_tokens, pages_per_seq, n_tokens,
+                    token_offset)))
+    return e;
+  if (topk < 1) return fail(ST_EINVAL, "topk positive; cache pages/offset must be block aligned");
+  if (topk > 4096) return fail(ST_EUNSUPPORTED, "st_sparse_pop: topk above 4096");
+  if (!q || !positions || !v || !ids || !top_scores || !log_zr || !out || !workspace)
+    return fail(ST_EINVAL, "st_sparse_pop: null pointer argument");
+  const size_t rows = (size_t)batch * queries * heads;
+  const size_t need =
+      align256(sizeof(float) * rows * (size_t)st::sparse_chunks((int)topk) * (st::sparse_dp((int)head_dim) + 2));
+  if (workspace_bytes < need)
+    return fail(ST_EINVAL, "st_sparse_pop: workspace of %zu bytes, %zu needed", workspace_bytes, need);
+  st::SparseArgs a;
+  fill_sparse(a, batch, queries, heads, head_dim, block_size, q, positions, k, v, page_table, page_tokens,
+              pages_per_seq, n_tokens, token_offset);
+  a.ids = const_cast<int64_t*>(ids);
+  a.top_scores = const_cast<float*>(top_scores);
+  a.log_zr = const_cast<float*>(log_zr);
+  a.topk = (int)topk;
+  a.out = out;
+  a.lse = lse;
+  a.partial = reinterpret_cast<float*>(workspace);
+  return launched(st::launch_sparse_pop(dtype, a, as_stream(stream)), "st_sparse_pop");
+}
+
+int st_sparse_fwd(int dtype, int64_t batch, int64_t queries, int64_t heads, int64_t head_dim,
+                  int64_t block_size, int64_t topk, const void* q, const int64_t* positions,
+                  const void* k, const void* v, const int32_t* page_table, int64_t page_tokens,
+                  int64_t pages_per_seq, int64_t n_tokens, int64_t token_offset, void* out,
+                  int64_t* ids, float* top_scores, float* log_zr, float* lse, void* workspace,
+                  size_t workspace_bytes, void* stream) {
+  int e;
+  if ((e = check_dtype(dtype)) || (e = check_sizes(batch, queries, 1, heads, head_dim, block_size)) ||
+      (e = check_envelope(head_dim, block_size)) ||
+      (e = check_kv("st_sparse_fwd", block_size, k, page_table, page_tokens, pages_per_seq, n_tokens,
+                    token_offset)))
+    return e;
+  if (topk < 1) return fail(ST_EINVAL, "topk positive; cache pages/offset must be block aligned");
+  if (topk > 4096) return fail(ST_EUNSUPPORTED, "st_sparse_fwd: topk above 4096");
+  if (!q || !positions || !v || !ids || !top_scores || !log_zr || !out || !workspace)
+    return fail(ST_EINVAL, "st_sparse_fwd: null pointer argument");
+  st::SparseArgs a;
+  fill_sparse(a, batch, queries, heads, head_dim, block_size, q, positions, k, v, page_table, page_tokens,
+              pages_per_seq, n_tokens, token_offset);
+  const size_t need = st_sparse_workspace_bytes(batch, queries, heads, head_dim, topk, a.n_blocks);
+  if (workspace_bytes < need)
+    return fail(ST_EINVAL, "st_sparse_fwd: workspace of %zu bytes, %zu needed", workspace_bytes, need);
+  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+    return fail(ST_EINVAL, "st_sparse_fwd: workspace must be 256-byte aligned");
+  const size_t rows = (size_t)batch * queries * heads;
+  a.scores = reinterpret_cast<float*>(workspace);
+  a.partial = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
+                                       align256(sizeof(float) * rows * (size_t)a.n_blocks));
+  a.ids = ids;
+  a.top_scores = top_scores;
+  a.log_zr = log_zr;
+  a.topk = (int)topk;
+  a.out = out;
+  a.lse = lse;
+  hipStream_t s = as_stream(stream);
+  hipError_t he = st::launch_sparse_scores(dtype, a, s);
+  if (he != hipSuccess) return launched(he, "st_sparse_fwd (scores)");
+  he = st::launch_sparse_select((int64_t)rows, a.n_blocks, a.topk, a.id_base, a.scores, ids, top_scores,
+                                log_zr, s);
+  if (he != hipSuccess) return launched(he, "st_sparse_fwd (select)");
+  return launched(st::launch_sparse_pop(dtype, a, s), "st_sparse_fwd (pop)");
+}
+
+}  // extern "C"

@@ -1,0 +1,473 @@
+// Paged sparse top-k inference forward (gfx950): block scores, exact top-k
+// selection and the gated sparse read.
+//
+// Semantics follow st/ops/sparse.py:15-174 and st/ops/kernels/sparse.py:9-113:
+//   s_j = logsumexp_{i in block j} q.k_i/sqrt(D) for visible blocks
+//   (j < p//b - 1, block complete inside the KV range), -inf otherwise;
+//   log Z_R = logsumexp_j s_j; ids = top-k of s (descending, ties by
+//   ascending block id, -1 for -inf); the output is the softmax over the
+//   local window (blocks p//b-1 and p//b, up to p) with logits a_i and the
+//   selected blocks with logits a_i + s_j - log Z_R.
+//
+// sparse_scores: one wave per (batch, head, 128-key chunk); S^T = K Q^T on
+//   MFMA with K fragments loaded straight from HBM (each key read once per
+//   32 queries), block logsumexp reduced in-lane.
+// sparse_select: one workgroup per (batch, query, head) row; exact radix
+//   select on the 64-bit key (ordered score, ~block id), then a rank sort.
+// sparse_pop: one wave per (row, block slot); online softmax over the block's
+//   tokens with coalesced 16-byte loads; sparse_merge combines the slots.
+#include "sparse.h"
+#include "tile.h"
+
+namespace st {
+
+// Token-row addressing of the KV view: pointer to token `t` (relative to
+// token_offset) of head h, and the element stride between consecutive tokens
+// of the same block (blocks never straddle pages).
+template <typename T, bool PAGED>
+__device__ __forceinline__ const T* kv_token(const KvView& kv, const T* base, int bi, int64_t t, int h,
+                                             int H, int D) {
+  if constexpr (PAGED) {
+    const int64_t lp = t / kv.page_tokens;
+    const int64_t page = kv.page_table[(int64_t)bi * kv.pages_per_seq + lp];
+    return base + ((page * H + h) * kv.page_tokens + (t - lp * kv.page_tokens)) * D;
+  } else {
+    return base + (((int64_t)bi * kv.n_tokens + t) * H + h) * D;
+  }
+}
+
+template <bool PAGED> __device__ __forceinline__ int64_t kv_stride(int H, int D) {
+  return PAGED ? (int64_t)D : (int64_t)H * D;
+}
+
+// ---------------------------------------------------------------------------
+template <typename T, int DP, bool PAGED>
+__global__ __launch_bounds__(256) void sparse_scores_kernel(SparseArgs a) {
+  typedef Mma<T> M;
+  typedef typename M::Frag Frag;
+  constexpr int NST = 4;  // 128 keys per wave
+  constexpr int NKC = DP / M::KW;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 31, half = lane >> 5;
+  const int h = blockIdx.y, bi = blockIdx.z;
+  const int64_t chunk = (int64_t)blockIdx.x * 4 + wave;
+  const int64_t t0 = chunk * 128;  // first token of the chunk, relative to token_offset
+  const int64_t n_tokens = a.kv.n_tokens;
+  if (t0 >= n_tokens) return;
+  const int b = a.block;
+  const int64_t first_block = t0 / b;               // chunk-local block 0, relative
+  const int nblk = 128 / b;                         // blocks in this chunk
+  const int64_t stride = kv_stride<PAGED>(a.H, a.D);
+  const T* kbase = reinterpret_cast<const T*>(a.kv.k);
+  const T* qbase = reinterpret_cast<const T*>(a.q);
+
+  for (int g0 = 0; g0 < a.Q; g0 += 32) {
+    const int row = g0 + col;
+    const bool row_in = row < a.Q;
+    const int64_t p = row_in ? a.pos[(int64_t)bi * a.Q + row] : -1;
+    // visible blocks are j < p//b - 1 (absolute); vis_lim is that limit in
+    // the scores array's numbering (block 0 = token_offset / b)
+    const int64_t vis_lim = p >= 0 ? p / b - 1 - a.id_base : -1;
+    // skip the chunk when no row of this group sees any of its blocks
+    float any = first_block < vis_lim ? 1.f : 0.f;
+    any = fmaxf(any, other_half(any));
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) any = fmaxf(any, __shfl_xor(any, off, 64));
+
+    float lse[NST][8];
+    if (any > 0.f) {
+      Frag qf[NKC];
+      const T* qrow = qbase + (((int64_t)bi * a.Q + (row_in ? row : 0)) * a.H + h) * a.D;
+#pragma unroll
+      for (int c = 0; c < NKC; ++c) {
+        const int d = c * M::KW + half * M::VEC;
+        qf[c] = (row_in && d < a.D) ? *reinterpret_cast<const Frag*>(qrow + d) : Frag{};
+      }
+      f32x16 s[NST];
+#pragma unroll
+      for (int st = 0; st < NST; ++st) {
+        int64_t t = t0 + 32 * st + col;
+        t = t < n_tokens ? t : n_tokens - 1;  // rows past the range are loaded clamped and masked below
+        const T* krow = kv_token<T, PAGED>(a.kv, kbase, bi, t, h, a.H, a.D);
+        f32x16 acc = zero16();
+#pragma unroll
+        for (int c = 0; c < NKC; ++c) {
+          const int d = c * M::KW + half * M::VEC;
+          const Frag kf = d < a.D ? *reinterpret_cast<const Frag*>(krow + d) : Frag{};
+          acc = M::mma(kf, qf[c], acc);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t tok = t0 + 32 * st + c_row(r, half);
+          acc[r] = tok < n_tokens ? acc[r] * a.scale_log2 : kNegInf;
+        }
+        s[st] = acc;
+      }
+      dispatch_logb(a.logb, [&]<int LOGB>() {
+        float mx[NST][8], sm[NST][8];
+        block_sums<NST, LOGB, OpMax>(s, mx);
+#pragma unroll
+        for (int st = 0; st < NST; ++st)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float m = mx[st][blk_slot<LOGB>(r)];
+            s[st][r] = m == kNegInf ? 0.f : fast_exp2(s[st][r] - m);
+          }
+        block_sums<NST, LOGB, OpAdd>(s, sm);
+#pragma unroll
+        for (int st = 0; st < NST; ++st)
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            lse[st][j] = (j < BlkSlots<LOGB>::n && sm[st][j] > 0.f) ? (mx[st][j] + fast_log2(sm[st][j])) * kLn2
+                                                                   : kNegInf;
+      });
+    }
+    if (!row_in) continue;
+    float* out = a.scores + (((int64_t)bi * a.Q + row) * a.H + h) * a.n_blocks;
+    dispatch_logb(a.logb, [&]<int LOGB>() {
+      if (!BlkSlots<LOGB>::per_half && half != 0) return;
+#pragma unroll
+      for (int st = 0; st < NST; ++st) {
+        if constexpr (LOGB >= 5) {
+          if ((32 * st) % (1 << LOGB) != 0) continue;  // one write per block
+        }
+#pragma unroll
+        for (int j = 0; j < BlkSlots<LOGB>::n; ++j) {
+          const int bl = blk_index<LOGB>(st, j, half);
+          if (bl >= nblk) continue;
+          const int64_t rel = first_block + bl;
+          if (rel >= a.n_blocks) continue;
+          const bool complete = (rel + 1) * b <= n_tokens;
+          const bool visible = complete && rel < vis_lim;
+          out[rel] = visible ? lse[st][j] : kNegInf;
+        }
+      }
+    });
+  }
+}
+
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t ordered_bits(float x) {
+  const uint32_t u = __float_as_uint(x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__global__ __launch_bounds__(256) void sparse_select_kernel(int64_t n_blocks, int topk, int64_t id_base,
+                                                            const float* scores, int64_t* ids, float* top,
+                                                            float* log_zr) {
+  __shared__ uint32_t hist[256];
+  __shared__ float red[8];
+  __shared__ uint64_t sel_key[4096];
+  __shared__ int sel_count;
+  __shared__ uint64_t prefix_sh;
+  __shared__ int64_t remaining_sh;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row = blockIdx.x;
+  const float* s = scores + row * n_blocks;
+
+  // log Z_R = logsumexp of the row
+  float mx = kNegInf;
+  for (int64_t i = tid; i < n_blocks; i += 256) mx = fmaxf(mx, s[i]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float sum = 0.f;
+  if (mx != kNegInf)
+    for (int64_t i = tid; i < n_blocks; i += 256) sum += __expf(s[i] - mx);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  if (lane == 0) red[4 + wave] = sum;
+  __syncthreads();
+  if (tid == 0) {
+    const float tot = red[4] + red[5] + red[6] + red[7];
+    log_zr[row] = (mx == kNegInf || !(tot > 0.f)) ? kNegInf : mx + __logf(tot);
+  }
+
+  // key = ordered score in the high word, inverted block id in the low word:
+  // larger key = higher score, then lower id. All keys are distinct.
+  auto key_of = [&](int64_t i) -> uint64_t {
+    return ((uint64_t)ordered_bits(s[i]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+  };
+  const int keep = (int64_t)topk < n_blocks ? topk : (int)n_blocks;
+  uint64_t kth = 0;  // smallest selected key
+  if ((int64_t)topk < n_blocks) {
+    if (tid == 0) { prefix_sh = 0; remaining_sh = topk; }
+    uint64_t mask = 0;
+    for (int pass = 0; pass < 8; ++pass) {
+      const int shift = 56 - 8 * pass;
+      hist[tid] = 0;
+      __syncthreads();
+      const uint64_t prefix = prefix_sh;
+      for (int64_t i = tid; i < n_blocks; i += 256) {
+        const uint64_t k = key_of(i);
+        if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+      }
+      __syncthreads();
+      if (tid == 0) {
+        int64_t rem = remaining_sh;
+        int d = 255;
+        for (; d > 0; --d) {
+          if ((int64_t)hist[d] >= rem) break;
+          rem -= hist[d];
+        }
+        remaining_sh = rem;
+        prefix_sh = prefix | ((uint64_t)d << shift);
+      }
+      mask |= (uint64_t)255 << shift;
+      __syncthreads();
+    }
+    kth = prefix_sh;
+  }
+
+  // gather the selected keys, then rank them (descending)
+  if (tid == 0) sel_count = 0;
+  __syncthreads();
+  for (int64_t i = tid; i < n_blocks; i += 256) {
+    const uint64_t k = key_of(i);
+    if (k >= kth) {
+      const int slot = atomicAdd(&sel_count, 1);
+      if (slot < 4096) sel_key[slot] = k;
+    }
+  }
+  __syncthreads();
+  const int cnt = sel_count < keep ? sel_count : keep;
+  int64_t* ids_row = ids + row * topk;
+  float* top_row = top + row * topk;
+  for (int i = tid; i < cnt; i += 256) {
+    const uint64_t k = sel_key[i];
+    int rank = 0;
+    for (int j = 0; j < cnt; ++j) rank += sel_key[j] > k ? 1 : 0;
+    const uint32_t idx = 0xffffffffu - (uint32_t)(k & 0xffffffffu);
+    const float sc = s[idx];
+    top_row[rank] = sc;
+    ids_row[rank] = sc == kNegInf ? -1 : (int64_t)idx + id_base;
+  }
+  for (int i = cnt + tid; i < topk; i += 256) {
+    top_row[i] = kNegInf;
+    ids_row[i] = -1;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pop: wave = one block slot of one row. Slots 0 and 1 are the local blocks
+// p//b - 1 and p//b, slot 2 + i is the i-th selected block.
+template <typename T, int DP, bool PAGED>
+__global__ __launch_bounds__(256) void sparse_pop_kernel(SparseArgs a) {
+  typedef typename Vec16<T>::type V;
+  constexpr int E = Vec16<T>::n;       // elements per 16-byte load
+  constexpr int LPT = DP / E;          // lanes per token
+  constexpr int TPI = 64 / LPT;        // tokens per load instruction
+  __shared__ float part_m[4], part_l[4];
+  __shared__ float part_o[4][DP];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t row = blockIdx.x;
+  const int h = (int)(row % a.H);
+  const int t = (int)((row / a.H) % a.Q);
+  const int bi = (int)(row / ((int64_t)a.H * a.Q));
+  const int slot = blockIdx.y * 4 + wave;
+  const int b = a.block;
+  const int64_t p = a.pos[(int64_t)bi * a.Q + t];
+  const int g = lane / LPT;            // token within an instruction
+  const int e0 = (lane % LPT) * E;     // first dimension of this lane
+
+  int64_t blk = -1;
+  float bias2 = 0.f;
+  bool ok = p >= 0 && slot < a.topk + 2;
+  if (ok) {
+    if (slot < 2) {
+      blk = p / b - 1 + slot;
+    } else {
+      blk = a.ids[row * a.topk + (slot - 2)];
+      const float sc = a.top_scores[row * a.topk + (slot - 2)];
+      float zr = a.log_zr[row];
+      zr = zr == kNegInf ? 0.f : zr;
+      ok = blk >= 0 && sc != kNegInf;
+      bias2 = (sc - zr) * kLog2e;
+    }
+    ok = ok && blk >= 0;
+  }
+  // tokens [lo, hi) of this block that are readable: inside the KV range and <= p
+  int64_t lo = 0, hi = 0;
+  if (ok) {
+    lo = blk * b;
+    hi = lo + b;
+    const int64_t r0 = a.kv.token_offset, r1 = a.kv.token_offset + a.kv.n_tokens;
+    lo = lo > r0 ? lo : r0;
+    hi = hi < r1 ? hi : r1;
+    hi = hi < p + 1 ? hi : p + 1;
+    if (hi <= lo) ok = false;
+  }
+
+  float q[E];
+  {
+    const T* qrow = reinterpret_cast<const T*>(a.q) + row * a.D;
+    V qv = {};
+    if (e0 < a.D) qv = load_vec<V>(qrow + e0);
+#pragma unroll
+    for (int e = 0; e < E; ++e) q[e] = to_float<T>(qv[e]) * a.scale_log2;
+  }
+  float m = kNegInf, l = 0.f, o[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) o[e] = 0.f;
+
+  if (ok) {
+    const int64_t stride = kv_stride<PAGED>(a.H, a.D);
+    const int64_t tb = blk * b - a.kv.token_offset;  // block start, range-relative
+    const int64_t tstart = (tb > 0 ? tb : 0);
+    const T* kb = kv_token<T, PAGED>(a.kv, reinterpret_cast<const T*>(a.kv.k), bi, tstart, h, a.H, a.D);
+    const T* vb = kv_token<T, PAGED>(a.kv, reinterpret_cast<const T*>(a.kv.v), bi, tstart, h, a.H, a.D);
+    const int ntok = (int)(hi - lo);  // tokens from tstart on (lo == tstart + token_offset)
+    for (int i0 = 0; i0 < ntok; i0 += TPI) {
+      const int i = i0 + g;
+      const bool valid = i < ntok;
+      V kv = {}, vv = {};
+      if (valid && e0 < a.D) {
+        kv = load_vec<V>(kb + (int64_t)i * stride + e0);
+        vv = load_vec<V>(vb + (int64_t)i * stride + e0);
+      }
+      float dot = 0.f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) dot += q[e] * to_float<T>(kv[e]);
+#pragma unroll
+      for (int off = 1; off < LPT; off <<= 1) dot += __shfl_xor(dot, off, 64);
+      const float x = valid ? dot + bias2 : kNegInf;
+      const float mn = fmaxf(m, x);
+      if (mn != kNegInf) {
+        const float alpha = fast_exp2(m - mn);
+        const float pw = fast_exp2(x - mn);
+        l = l * alpha + pw;
+#pragma unroll
+        for (int e = 0; e < E; ++e) o[e] = o[e] * alpha + pw * to_float<T>(vv[e]);
+        m = mn;
+      }
+    }
+  }
+  // merge the TPI token groups (lanes e0-aligned, differing in g)
+#pragma unroll
+  for (int off = LPT; off < 64; off <<= 1) {
+    const float m2 = __shfl_xor(m, off, 64);
+    const float l2 = __shfl_xor(l, off, 64);
+    const float mn = fmaxf(m, m2);
+    const float a1 = mn == kNegInf ? 0.f : fast_exp2(m - mn);
+    const float a2 = mn == kNegInf ? 0.f : fast_exp2(m2 - mn);
+    l = l * a1 + l2 * a2;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float o2 = __shfl_xor(o[e], off, 64);
+      o[e] = o[e] * a1 + o2 * a2;
+    }
+    m = mn;
+  }
+  if (lane < LPT) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) part_o[wave][e0 + e] = o[e];
+    if (lane == 0) { part_m[wave] = m; part_l[wave] = l; }
+  }
+  __syncthreads();
+  // workgroup partial: merge the 4 waves
+  const int64_t chunks = gridDim.y;
+  float* dst = a.partial + (row * chunks + blockIdx.y) * (DP + 2);
+  float mm = fmaxf(fmaxf(part_m[0], part_m[1]), fmaxf(part_m[2], part_m[3]));
+  float w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = mm == kNegInf ? 0.f : fast_exp2(part_m[i] - mm);
+  for (int d = threadIdx.x; d < DP; d += 256)
+    dst[2 + d] = w[0] * part_o[0][d] + w[1] * part_o[1][d] + w[2] * part_o[2][d] + w[3] * part_o[3][d];
+  if (threadIdx.x == 0) {
+    dst[0] = mm;
+    dst[1] = w[0] * part_l[0] + w[1] * part_l[1] + w[2] * part_l[2] + w[3] * part_l[3];
+  }
+}
+
+template <typename T, int DP>
+__global__ __launch_bounds__(64) void sparse_merge_kernel(SparseArgs a, int chunks) {
+  const int64_t row = blockIdx.x;
+  const int lane = threadIdx.x;
+  const float* src = a.partial + row * chunks * (DP + 2);
+  float mm = kNegInf;
+  for (int c = 0; c < chunks; ++c) mm = fmaxf(mm, src[c * (DP + 2)]);
+  float l = 0.f;
+  float o[DP / 64];
+#pragma unroll
+  for (int j = 0; j < DP / 64; ++j) o[j] = 0.f;
+  for (int c = 0; c < chunks; ++c) {
+    const float* pc = src + c * (DP + 2);
+    const float w = mm == kNegInf ? 0.f : fast_exp2(pc[0] - mm);
+    l += w * pc[1];
+#pragma unroll
+    for (int j = 0; j < DP / 64; ++j) o[j] += w * pc[2 + lane + 64 * j];
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  T* out = reinterpret_cast<T*>(a.out) + row * a.D;
+#pragma unroll
+  for (int j = 0; j < DP / 64; ++j) {
+    const int d = lane + 64 * j;
+    if (d < a.D) out[d] = from_float<T>(o[j] * inv);
+  }
+  if (a.lse && lane == 0) a.lse[row] = (l > 0.f && mm != kNegInf) ? (mm + fast_log2(l)) * kLn2 : kNegInf;
+}
+
+// ---------------------------------------------------------------------------
+template <typename T, int DP>
+static hipError_t scores_dp(const SparseArgs& a, hipStream_t s) {
+  const int64_t chunks = (a.kv.n_tokens + 127) / 128;
+  dim3 grid((unsigned)((chunks + 3) / 4), a.H, a.B);
+  if (a.kv.page_table) hipLaunchKernelGGL((sparse_scores_kernel<T, DP, true>), grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((sparse_scores_kernel<T, DP, false>), grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t scores_t(const SparseArgs& a, hipStream_t s) {
+  if (a.D <= 64) return scores_dp<T, 64>(a, s);
+  if (a.D <= 128) return scores_dp<T, 128>(a, s);
+  return scores_dp<T, 256>(a, s);
+}
+
+hipError_t launch_sparse_scores(int dtype, const SparseArgs& a, hipStream_t stream) {
+  switch (dtype) {
+    case 2: return scores_t<bf16>(a, stream);
+    case 1: return scores_t<f16>(a, stream);
+    default: return scores_t<float>(a, stream);
+  }
+}
+
+hipError_t launch_sparse_select(int64_t rows, int64_t n_blocks, int topk, int64_t id_base,
+                                const float* scores, int64_t* ids, float* top, float* log_zr,
+                                hipStream_t stream) {
+  hipLaunchKernelGGL(sparse_select_kernel, dim3((unsigned)rows), dim3(256), 0, stream, n_blocks, topk, id_base,
+                     scores, ids, top, log_zr);
+  return hipGetLastError();
+}
+
+template <typename T, int DP>
+static hipError_t pop_dp(const SparseArgs& a, hipStream_t s) {
+  const int64_t rows = (int64_t)a.B * a.Q * a.H;
+  const int chunks = (int)sparse_chunks(a.topk);
+  dim3 grid((unsigned)rows, chunks);
+  if (a.kv.page_table) hipLaunchKernelGGL((sparse_pop_kernel<T, DP, true>), grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((sparse_pop_kernel<T, DP, false>), grid, dim3(256), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((sparse_merge_kernel<T, DP>), dim3((unsigned)rows), dim3(64), 0, s, a, chunks);
+  return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t pop_t(const SparseArgs& a, hipStream_t s) {
+  if (a.D <= 64) return pop_dp<T, 64>(a, s);
+  if (a.D <= 128) return pop_dp<T, 128>(a, s);
+  return pop_dp<T, 256>(a, s);
+}
+
+hipError_t launch_sparse_pop(int dtype, const SparseArgs& a, hipStream_t stream) {
+  switch (dtype) {
+    case 2: return pop_t<bf16>(a, stream);
+    case 1: return pop_t<f16>(a, stream);
+    default: return pop_t<float>(a, stream);
+  }
+}
+
+}  // namespace st

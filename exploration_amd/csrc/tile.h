@@ -1,0 +1,238 @@
+// Tile building blocks shared by the dense forward and backward kernels:
+// LDS staging of key/value tiles, MFMA products in the transposed layout and
+// per-(row, key block) reductions.
+#pragma once
+
+#include "common.h"
+
+namespace st {
+
+// LDS row strides (elements). Row-major tiles pad 16 bytes per row;
+// transposed 16-bit tiles pad 8 bytes so that 32 lanes reading 8 bytes from
+// 32 consecutive rows hit distinct banks.
+template <typename T, int DP> struct RowLd { static constexpr int value = DP + 16 / (int)sizeof(T); };
+template <int NT> struct TLd { static constexpr int value = NT + 4; };
+
+template <typename T> struct Vec16;
+template <> struct Vec16<bf16> { typedef bf16x8 type; static constexpr int n = 8; };
+template <> struct Vec16<f16> { typedef f16x8 type; static constexpr int n = 8; };
+template <> struct Vec16<float> { typedef f32x4 type; static constexpr int n = 4; };
+
+// Copy rows [r0, r0+ROWS) x columns [0, DP) of a [*, stride] matrix into LDS
+// (row-major, stride LD), zero-filling rows >= nrows and columns >= ncols.
+// ncols must be a multiple of 16 bytes worth of elements.
+template <typename T, int ROWS, int DP, int LD, int NTHREADS>
+__device__ __forceinline__ void stage_rows(T* lds, const T* g, int64_t stride, int r0, int nrows,
+                                           int ncols) {
+  typedef typename Vec16<T>::type V;
+  constexpr int E = Vec16<T>::n;
+  constexpr int CPR = DP / E;
+  constexpr int TOTAL = ROWS * CPR;
+#pragma unroll
+  for (int it = 0; it < (TOTAL + NTHREADS - 1) / NTHREADS; ++it) {
+    const int id = threadIdx.x + it * NTHREADS;
+    if (TOTAL % NTHREADS != 0 && id >= TOTAL) break;
+    const int n = id / CPR, c = (id % CPR) * E;
+    V val = {};
+    if (r0 + n < nrows && c < ncols) val = load_vec<V>(g + (int64_t)(r0 + n) * stride + c);
+    *reinterpret_cast<V*>(lds + n * LD + c) = val;
+  }
+}
+
+// Same source, stored transposed: lds[c][n] (stride LDT) for 16-bit types.
+template <typename T, int ROWS, int DP, int LDT, int NTHREADS>
+__device__ __forceinline__ void stage_rows_t(T* lds, const T* g, int64_t stride, int r0, int nrows,
+                                             int ncols) {
+  typedef typename Vec16<T>::type V;
+  constexpr int E = Vec16<T>::n;
+  constexpr int CPR = DP / E;
+  constexpr int TOTAL = ROWS * CPR;
+#pragma unroll
+  for (int it = 0; it < (TOTAL + NTHREADS - 1) / NTHREADS; ++it) {
+    const int id = threadIdx.x + it * NTHREADS;
+    if (TOTAL % NTHREADS != 0 && id >= TOTAL) break;
+    const int n = id % ROWS, c = (id / ROWS) * E;
+    V val = {};
+    if (r0 + n < nrows && c < ncols) val = load_vec<V>(g + (int64_t)(r0 + n) * stride + c);
+#pragma unroll
+    for (int e = 0; e < E; ++e) lds[(c + e) * LDT + n] = val[e];
+  }
+}
+
+// Operand fragment for row `row` of a row-major LDS tile, contraction chunk c:
+// elements [c*KW + half*VEC, +VEC).
+template <typename T, int LD>
+__device__ __forceinline__ typename Mma<T>::Frag frag_row(const T* lds, int row, int c, int half) {
+  typedef typename Mma<T>::Frag F;
+  return *reinterpret_cast<const F*>(lds + row * LD + c * Mma<T>::KW + half * Mma<T>::VEC);
+}
+
+// Operand fragment from a transposed 16-bit LDS tile (lds[r][key]) for row r
+// and the 16 keys [k0, k0+16) in the permuted order that matches the C-tile
+// layout: slots 0..3 <-> k0+4h+{0..3}, slots 4..7 <-> k0+8+4h+{0..3}.
+template <typename T, int LDT>
+__device__ __forceinline__ typename Mma<T>::Frag frag_t16(const T* lds, int r, int k0, int half) {
+  typedef T V4 __attribute__((ext_vector_type(4)));
+  const T* p = lds + r * LDT + k0 + 4 * half;
+  V4 lo = *reinterpret_cast<const V4*>(p);
+  V4 hi = *reinterpret_cast<const V4*>(p + 8);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// B-operand fragment (16-bit) from C-tile registers [8*c2, 8*c2+8) of x.
+template <typename T>
+__device__ __forceinline__ typename Mma<T>::Frag frag_from_c(const f32x16& x, int c2) {
+  typename Mma<T>::Frag f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = from_float<T>(x[8 * c2 + e]);
+  return f;
+}
+
+// S^T tile (NT keys x 32 rows) = K_tile . Q^T with K staged row-major in LDS
+// (stride LDK) and Q^T held in registers as fragments qf[DP/KW].
+template <typename T, int NST, int NKC, int LDK>
+__device__ __forceinline__ void scores_t(f32x16 (&s)[NST], const T* lds_k,
+                                         const typename Mma<T>::Frag (&qf)[NKC], int col, int half) {
+#pragma unroll
+  for (int st = 0; st < NST; ++st) {
+    f32x16 acc = zero16();
+#pragma unroll
+    for (int c = 0; c < NKC; ++c) acc = Mma<T>::mma(frag_row<T, LDK>(lds_k, 32 * st + col, c, half), qf[c], acc);
+    s[st] = acc;
+  }
+}
+
+// acc^T[d][row] += X^T . P^T where P is given as C tiles p[NST] (keys x rows)
+// and X (values or keys) is staged in LDS: transposed [DP][LDT] for 16-bit
+// types, row-major [NT][LD] for fp32.
+template <typename T, int NST, int NDT, int LDX>
+__device__ __forceinline__ void accumulate_t(f32x16 (&acc)[NDT], const f32x16 (&p)[NST], const T* lds_x,
+                                             int col, int half) {
+  if constexpr (sizeof(T) == 2) {
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+#pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2) {
+        const typename Mma<T>::Frag b = frag_from_c<T>(p[st], c2);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+          acc[dt] = Mma<T>::mma(frag_t16<T, LDX>(lds_x, 32 * dt + col, 32 * st + 16 * c2, half), b, acc[dt]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        const int key = 32 * st + c_row(t, half);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+          acc[dt] = Mma<T>::mma(lds_x[key * LDX + 32 * dt + col], p[st][t], acc[dt]);
+      }
+    }
+  }
+}
+
+// Per-(row, key block) sums of x over the keys of each block, for a tile of
+// NST C tiles with block size 2^LOGB (the tile holds whole blocks). blk[st][j]
+// receives the sum of block slot j of subtile st; blk_slot maps a register
+// to its slot. For LOGB >= 5 every subtile of a block gets the block total.
+template <int LOGB> __device__ __forceinline__ constexpr int blk_slot(int r) {
+  return LOGB == 1 ? (r >> 1) : (LOGB <= 3 ? (r >> 2) : (LOGB == 4 ? (r >> 3) : 0));
+}
+
+struct OpAdd {
+  static __device__ __forceinline__ float f(float x, float y) { return x + y; }
+  static __device__ __forceinline__ float other(float x) { return other_half(x); }
+};
+struct OpMax {
+  static __device__ __forceinline__ float f(float x, float y) { return fmaxf(x, y); }
+  static __device__ __forceinline__ float other(float x) { return other_half(x); }
+};
+
+template <int NST, int LOGB, typename Op = OpAdd>
+__device__ __forceinline__ void block_sums(const f32x16 (&x)[NST], float (&blk)[NST][8]) {
+  if constexpr ((1 << LOGB) > 32 * NST) {
+    // block larger than the tile: never dispatched (tiles hold whole blocks)
+  } else if constexpr (LOGB >= 5) {
+    constexpr int G = (1 << LOGB) / 32;  // subtiles per block
+    float t[NST];
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+      float acc = x[st][0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) acc = Op::f(acc, x[st][r]);
+      t[st] = acc;
+    }
+#pragma unroll
+    for (int st = 0; st < NST; ++st) t[st] = Op::f(t[st], Op::other(t[st]));
+#pragma unroll
+    for (int g0 = 0; g0 < NST; g0 += G) {
+      float tot = t[g0];
+#pragma unroll
+      for (int g = 1; g < G; ++g) tot = Op::f(tot, t[g0 + g]);
+#pragma unroll
+      for (int g = 0; g < G; ++g) blk[g0 + g][0] = tot;
+    }
+  } else if constexpr (LOGB == 4) {
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+      float a0 = x[st][0], a1 = x[st][8];
+#pragma unroll
+      for (int r = 1; r < 8; ++r) { a0 = Op::f(a0, x[st][r]); a1 = Op::f(a1, x[st][r + 8]); }
+      blk[st][0] = Op::f(a0, Op::other(a0));
+      blk[st][1] = Op::f(a1, Op::other(a1));
+    }
+  } else if constexpr (LOGB == 3) {
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float a = Op::f(Op::f(x[st][4 * i], x[st][4 * i + 1]), Op::f(x[st][4 * i + 2], x[st][4 * i + 3]));
+        blk[st][i] = Op::f(a, Op::other(a));
+      }
+    }
+  } else if constexpr (LOGB == 2) {
+#pragma unroll
+    for (int st = 0; st < NST; ++st)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        blk[st][i] = Op::f(Op::f(x[st][4 * i], x[st][4 * i + 1]), Op::f(x[st][4 * i + 2], x[st][4 * i + 3]));
+  } else {
+#pragma unroll
+    for (int st = 0; st < NST; ++st)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) blk[st][i] = Op::f(x[st][2 * i], x[st][2 * i + 1]);
+  }
+}
+
+// Index, within the tile, of the key block that slot j of subtile st in a
+// lane of half h refers to (block size 2^LOGB, NST subtiles of 32 keys).
+template <int LOGB> __device__ __forceinline__ int blk_index(int st, int j, int h) {
+  if constexpr (LOGB >= 5) return (32 * st) >> LOGB;
+  else if constexpr (LOGB == 4) return 2 * st + j;
+  else if constexpr (LOGB == 3) return 4 * st + j;
+  else if constexpr (LOGB == 2) return 8 * st + 2 * j + h;
+  else return 16 * st + 4 * (j >> 1) + 2 * h + (j & 1);
+}
+// Slots per subtile that carry distinct blocks, and whether the two halves of
+// the wave hold different blocks (block size <= 4).
+template <int LOGB> struct BlkSlots {
+  static constexpr int n = LOGB >= 5 ? 1 : (LOGB == 4 ? 2 : (LOGB >= 2 ? 4 : 8));
+  static constexpr bool per_half = LOGB <= 2;
+};
+
+// Runs body.template operator()<LOGB>() for the runtime block size.
+template <typename F> __device__ __forceinline__ void dispatch_logb(int logb, F&& body) {
+  switch (logb) {
+    case 1: body.template operator()<1>(); break;
+    case 2: body.template operator()<2>(); break;
+    case 3: body.template operator()<3>(); break;
+    case 4: body.template operator()<4>(); break;
+    case 5: body.template operator()<5>(); break;
+    case 6: body.template operator()<6>(); break;
+    default: body.template operator()<7>(); break;
+  }
+}
+
+}  // namespace st

@@ -1,0 +1,130 @@
+/*
+ * st_attn.h: C ABI of the MI355X (gfx950) Stack attention kernels.
+ *
+ * A drop-in for the GPU kernel layer of zhjerry25/Exploration (package `st`):
+ * each entry point replaces the Triton launch(es) named in its comment. All
+ * tensors are device pointers to contiguous row-major arrays; the caller owns
+ * every buffer (these functions never allocate, free or synchronise) and
+ * passes the HIP stream to launch on (NULL = the legacy default stream).
+ *
+ * Return value: ST_OK, or a status whose message st_last_error() returns
+ * (thread-local). ST_EINVAL and ST_EUNSUPPORTED correspond to the reference's
+ * ValueError (st/ops/attention.py:155-162,171-172; st/ops/sparse.py:108-110),
+ * ST_ELAUNCH to a RuntimeError carrying the HIP error string.
+ *
+ * Layouts (reference docs/API.md:154):
+ *   q, out, rc, dout, dq    [B, Q, H, D]   element type `dtype`, rc float
+ *   k, v, dk, dv            [B, N, H, D]
+ *   positions               [B, Q] int64, absolute key index, -1 = padding row
+ *   pr, zr, z, log_zr, lse  [B, Q, H] float
+ *   block scores            [B, Q, H, G] float, G = blocks of the KV range
+ *   ids / top scores        [B, Q, H, topk] int64 / float
+ * Paged KV (no reference counterpart; the reference slices contiguous pages,
+ * st/ops/sparse.py:75-96): pool [P, H, page_tokens, D] addressed through
+ * page_table [B, pages_per_seq] int32 (logical page -> pool page).
+ */
+#ifndef ST_ATTN_H
+#define ST_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ST_ABI_VERSION 1
+
+#define ST_DTYPE_F32 0
+#define ST_DTYPE_F16 1
+#define ST_DTYPE_BF16 2
+
+#define ST_OK 0
+#define ST_EINVAL 1
+#define ST_EUNSUPPORTED 2
+#define ST_ELAUNCH 3
+
+/* Version of this ABI (ST_ABI_VERSION). */
+int st_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* st_last_error(void);
+
+/* 1 if the fused kernels support (dtype, head_dim, block_size), else 0.
+ * Replaces the Triton capability predicate triton_supported
+ * (st/ops/attention.py:142-145): fp32/fp16/bf16, block a power of two in
+ * [2, 128], head_dim <= 256 (here also a multiple of 8). */
+int st_dense_supported(int dtype, int64_t head_dim, int64_t block_size);
+
+/* Gated dense forward. Replaces the `_forward` launch of
+ * st/ops/kernels/dense.py:197-217 (kernel st/ops/kernels/dense.py:32-86).
+ * Writes out (dtype) and the saved statistics rc, pr, zr, z (float). */
+int st_dense_fwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_t heads,
+                 int64_t head_dim, int64_t block_size, const void* q, const void* k,
+                 const void* v, const int64_t* positions, void* out, float* rc, float* pr,
+                 float* zr, float* z, void* stream);
+
+/* Bytes of device workspace st_dense_bwd needs (delta and rho). */
+size_t st_dense_bwd_workspace_bytes(int64_t batch, int64_t queries, int64_t heads);
+
+/* Gated dense backward (first derivatives). Replaces the `_preprocess`,
+ * `_backward_q` and `_backward_kv` launches of st/ops/kernels/dense.py:221-233.
+ * Inputs are the forward's inputs and saved statistics plus dout; writes
+ * dq, dk, dv in `dtype`. */
+int st_dense_bwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_t heads,
+                 int64_t head_dim, int64_t block_size, const void* q, const void* k,
+                 const void* v, const int64_t* positions, const void* out, const float* rc,
+                 const float* pr, const float* zr, const float* z, const void* dout, void* dq,
+                 void* dk, void* dv, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Exact block scores s_j = logsumexp over block j of q.k/sqrt(D) for the
+ * blocks [token_offset/b, token_offset/b + n_blocks) with the reference's
+ * visibility mask (-inf unless j < p//b - 1 and the block lies inside the KV
+ * range). Replaces block_scores / `_scores`
+ * (st/ops/kernels/sparse.py:9-35,81-100). KV addressing: page_table == NULL
+ * means contiguous k[B, n_tokens, H, D] holding absolute tokens
+ * [token_offset, token_offset + n_tokens); otherwise the paged pool. */
+int st_sparse_scores(int dtype, int64_t batch, int64_t queries, int64_t heads, int64_t head_dim,
+                     int64_t block_size, const void* q, const int64_t* positions, const void* k,
+                     const int32_t* page_table, int64_t page_tokens, int64_t pages_per_seq,
+                     int64_t n_tokens, int64_t token_offset, float* scores, int64_t n_blocks,
+                     void* stream);
+
+/* Top-k blocks per row of scores [rows, n_blocks]: ids (block index +
+ * id_base, -1 where the score is -inf) and scores in descending order, ties
+ * by ascending block id, plus log_zr = logsumexp of the row. Replaces the
+ * running top-k and log Z_R of st/ops/sparse.py:121-139,154. */
+int st_sparse_select(int64_t rows, int64_t n_blocks, int64_t topk, int64_t id_base,
+                     const float* scores, int64_t* ids, float* top_scores, float* log_zr,
+                     void* stream);
+
+/* Bytes of device workspace st_sparse_pop / st_sparse_fwd need. */
+size_t st_sparse_workspace_bytes(int64_t batch, int64_t queries, int64_t heads, int64_t head_dim,
+                                 int64_t topk, int64_t n_blocks);
+
+/* Softmax read over the local window and the selected blocks, gated by
+ * log_zr. Replaces sparse_pop / `_pop` and the LSE merge of
+ * st/ops/kernels/sparse.py:38-78,103-113 and st/ops/sparse.py:157-162.
+ * Writes out (dtype) and, if lse != NULL, the row logsumexp (float). */
+int st_sparse_pop(int dtype, int64_t batch, int64_t queries, int64_t heads, int64_t head_dim,
+                  int64_t block_size, const void* q, const int64_t* positions, const void* k,
+                  const void* v, const int32_t* page_table, int64_t page_tokens,
+                  int64_t pages_per_seq, int64_t n_tokens, int64_t token_offset,
+                  const int64_t* ids, const float* top_scores, const float* log_zr, int64_t topk,
+                  void* out, float* lse, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Whole sparse forward: scores, selection and read in one call
+ * (st/ops/sparse.py:99-174 on one device). ids/top_scores/log_zr receive
+ * the selection; scores of all n_blocks blocks live in the workspace. */
+int st_sparse_fwd(int dtype, int64_t batch, int64_t queries, int64_t heads, int64_t head_dim,
+                  int64_t block_size, int64_t topk, const void* q, const int64_t* positions,
+                  const void* k, const void* v, const int32_t* page_table, int64_t page_tokens,
+                  int64_t pages_per_seq, int64_t n_tokens, int64_t token_offset, void* out,
+                  int64_t* ids, float* top_scores, float* log_zr, float* lse, void* workspace,
+                  size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ST_ATTN_H */

@@ -1,0 +1,109 @@
+"""C ABI checks that need no GPU: the library loads, exports every function
+include/st_attn.h declares, reports its version, and rejects bad arguments
+with the reference's error classes before any device work."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from exploration_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "st_attn.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(st_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declarations_are_bound():
+    names = declared_functions()
+    assert len(names) >= 10
+    assert set(names) == set(_lib.SIGNATURES), "ctypes binding and header disagree"
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} missing from libst_attn.so"
+    assert lib.st_abi_version() == 1
+    assert lib.st_last_error() == b""
+
+
+def test_support_predicate():
+    lib = _lib.load()
+    for dtype in (0, 1, 2):
+        for b in (2, 4, 16, 64, 128):
+            assert lib.st_dense_supported(dtype, 128, b) == 1
+        assert lib.st_dense_supported(dtype, 128, 3) == 0
+        assert lib.st_dense_supported(dtype, 128, 256) == 0
+        assert lib.st_dense_supported(dtype, 264, 64) == 0
+        assert lib.st_dense_supported(dtype, 6, 64) == 0
+    assert lib.st_dense_supported(7, 64, 64) == 0
+
+
+def test_argument_errors_map_to_value_error():
+    """Argument checks run on the host and fail before any HIP call."""
+    lib = _lib.load()
+    null = None
+    status = lib.st_dense_fwd(2, 1, 1, 1, 1, 64, 16, *([null] * 3), null, null, *([null] * 4), null)
+    assert status == _lib.ST_EINVAL
+    assert b"null pointer" in lib.st_last_error()
+    with pytest.raises(ValueError, match="null pointer"):
+        _lib.check(status, lib)
+    status = lib.st_dense_fwd(2, 1, 1, 1, 1, 64, 3, *([null] * 3), null, null, *([null] * 4), null)
+    assert status == _lib.ST_EUNSUPPORTED
+    with pytest.raises(ValueError, match="power of two"):
+        _lib.check(status, lib)
+    status = lib.st_dense_fwd(2, 0, 1, 1, 1, 64, 16, *([null] * 3), null, null, *([null] * 4), null)
+    assert status == _lib.ST_EINVAL
+    status = lib.st_sparse_select(4, 10, 0, 0, null, null, null, null, null)
+    assert status == _lib.ST_EINVAL
+    assert b"topk positive" in lib.st_last_error()
+    status = lib.st_sparse_fwd(2, 1, 1, 1, 64, 16, 4, null, null, ctypes.c_void_p(16), null, null, 16, 1,
+                               100, 8, null, null, null, null, null, null, 0, null)
+    assert status == _lib.ST_EINVAL and b"block aligned" in lib.st_last_error()
+    assert lib.st_dense_bwd_workspace_bytes(2, 5, 3) == 2 * 256
+
+
+def test_python_entry_points_validate_like_the_reference():
+    from exploration_amd import TensorPages, dense_attention, sparse_attention
+    q = torch.zeros(1, 2, 1, 8)
+    k = torch.zeros(1, 4, 1, 8)
+    pos = torch.zeros(1, 2, dtype=torch.long)
+    with pytest.raises(ValueError, match="unknown attention backend"):
+        dense_attention(q, k, k, pos, 2, backend="cuda")
+    with pytest.raises(ValueError, match="expected q"):
+        dense_attention(q, k, k[:, :3], pos, 2)
+    with pytest.raises(ValueError, match="dimensions differ"):
+        dense_attention(q, k[:, :, :, :4], k[:, :, :, :4], pos, 2)
+    with pytest.raises(ValueError, match="positive"):
+        dense_attention(q, k, k, pos, 0)
+    with pytest.raises(ValueError, match="HIP kernels"):
+        dense_attention(q, k, k, pos, 2)  # CPU tensors: no fallback
+    with pytest.raises(ValueError, match="topk positive"):
+        sparse_attention(q, TensorPages(k, k, 4), pos, 2, 0)
+    with pytest.raises(ValueError, match="block aligned"):
+        sparse_attention(q, TensorPages(k, k, 3), pos, 2, 1)
+
+
+def test_paged_cache_layout_round_trip():
+    from exploration_amd import PagedKV
+    g = torch.Generator().manual_seed(0)
+    k = torch.randn(2, 37, 3, 8, generator=g)
+    v = torch.randn(2, 37, 3, 8, generator=g)
+    table = torch.randperm(2 * 5, generator=g).reshape(2, 5)
+    cache = PagedKV.from_dense(k, v, 8, table)
+    assert cache.k_pool.shape == (10, 3, 8, 8)
+    # token t of batch b, head h lives at pool[table[b, t//8], h, t%8]
+    for b, t, h in ((0, 0, 0), (1, 36, 2), (0, 17, 1)):
+        assert torch.equal(cache.k_pool[table[b, t // 8], h, t % 8], k[b, t, h])
+    kk, vv = cache.gather(5, 30)
+    assert torch.equal(kk, k[:, 5:30]) and torch.equal(vv, v[:, 5:30])
+    pages = list(cache.pages("cpu"))
+    assert [p[0] for p in pages] == [0, 8, 16, 24, 32]
+    assert torch.equal(torch.cat([p[1] for p in pages], 1), k)

@@ -1,0 +1,127 @@
+"""Dense gated attention: HIP kernels against the oracle on identical inputs.
+
+Cases follow the reference's GPU validation matrix
+(st/tools/validate.py:75-118: seed 772, q [2,5,2,D], positions with early,
+block-boundary, last and padding rows) plus the BASELINE configurations:
+cfg2 (bf16, B1 H8 N=Q=4096 D128 b128) at full size, cfg3 (fp32 ragged tail),
+and a cfg5-shaped chunk (b16 D64). Tolerances: tests/helpers.py.
+"""
+import math
+
+import pytest
+import torch
+
+from exploration_amd import _lib, dense_attention, launch_report
+from exploration_amd.attention import dense_forward_stats
+from exploration_amd.workloads import CFG2, CFG3, dense_config
+from oracle import dense as od
+from tests.helpers import assert_close, error_metrics
+
+pytestmark = pytest.mark.gpu
+
+VALIDATE_CASES = [(17, 2, 16), (129, 16, 32), (257, 32, 64), (193, 64, 96), (385, 128, 128),
+                  (131, 16, 256), (385, 128, 256)]
+DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+
+
+def _validate_case(n, b, d, dtype, seed=772):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(2, 5, 2, d, generator=g).to(dtype)
+    k = torch.randn(2, n, 2, d, generator=g).to(dtype)
+    v = torch.randn(2, n, 2, d, generator=g).to(dtype)
+    probe = torch.randn(2, 5, 2, d, generator=g).to(dtype)
+    pos = torch.tensor([[0, b - 1, min(2 * b + 1, n - 1), n - 1, -1], [n - 1, 0, n // 2, -1, n - 2]])
+    return q, k, v, pos, probe
+
+
+def _check_dense(q, k, v, pos, probe, b, device, dtype, oracle_device="cpu", label=""):
+    """Forward output, saved statistics and all input gradients against the
+    oracle (float64 on CPU, float32 when run on the GPU for large shapes)."""
+    work = torch.float64 if oracle_device == "cpu" else torch.float32
+    qo, ko, vo = (t.to(oracle_device, work) for t in (q, k, v))
+    po, go = pos.to(oracle_device), probe.to(oracle_device, work)
+    stats = od.forward_stats(qo, ko, vo, po, b)
+    grads = od.backward_explicit(qo, ko, vo, po, b, go, stats)
+
+    qg, kg, vg = (t.to(device).requires_grad_() for t in (q, k, v))
+    out = dense_attention(qg, kg, vg, pos.to(device), b)
+    dq, dk, dv = torch.autograd.grad(out, (qg, kg, vg), probe.to(device))
+    hip_stats = dense_forward_stats(qg.detach(), kg.detach(), vg.detach(), pos.to(device), b)
+    torch.cuda.synchronize()
+    report = {name: error_metrics(a, e) for name, a, e in
+              zip(("out", "dq", "dk", "dv"), (out, dq, dk, dv), (stats[0],) + tuple(grads))}
+    print(f"{label} {dtype} errors {report}", flush=True)
+    assert_close(out, stats[0], dtype, f"{label} out")
+    assert torch.equal(hip_stats[0], out.detach())
+    stat_dtype = torch.float32 if dtype == torch.float32 else dtype
+    for name, a, e in zip(("rc", "pr", "zr", "z"), hip_stats[1:], stats[1:]):
+        assert_close(a, e, stat_dtype, f"{label} {name}")
+    for name, a, e in zip(("dq", "dk", "dv"), (dq, dk, dv), grads):
+        assert_close(a, e, dtype, f"{label} {name}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("n,b,d", VALIDATE_CASES)
+def test_validation_matrix(device, n, b, d, dtype):
+    print(f"dense case n={n} b={b} d={d} {dtype}", flush=True)
+    q, k, v, pos, probe = _validate_case(n, b, d, dtype)
+    _check_dense(q, k, v, pos, probe, b, device, dtype, label=f"n={n} b={b} d={d}")
+
+
+def test_cfg3_fp32_ragged_tail(device):
+    """cfg3: fp32, B1 H4, N=385, queries at 380..384, D=128, b=128; the last
+    key block holds one token."""
+    print("dense cfg3", flush=True)
+    q, k, v, pos, do, b = dense_config(CFG3)
+    assert pos.tolist() == [[380, 381, 382, 383, 384]]
+    _check_dense(q, k, v, pos, do, b, device, torch.float32, label="cfg3")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
+def test_unsorted_positions_and_padding(device, dtype):
+    """Arbitrary (unsorted, repeated, padding) positions over several query
+    tiles, batch 2, N not a multiple of any tile."""
+    print(f"dense unsorted {dtype}", flush=True)
+    g = torch.Generator().manual_seed(5)
+    n, b, d = 1000, 32, 64
+    q = torch.randn(2, 150, 3, d, generator=g).to(dtype)
+    k = torch.randn(2, n, 3, d, generator=g).to(dtype)
+    v = torch.randn(2, n, 3, d, generator=g).to(dtype)
+    probe = torch.randn(2, 150, 3, d, generator=g).to(dtype)
+    pos = torch.randint(-1, n, (2, 150), generator=g)
+    _check_dense(q, k, v, pos, probe, b, device, dtype, label="unsorted")
+
+
+def test_cfg5_shaped_chunk(device):
+    """cfg5 G-round shape: bf16, H16 D64 b16, 240 supervised query positions
+    over N=8192 keys (oracle in float32 on the GPU)."""
+    print("dense cfg5 chunk", flush=True)
+    g = torch.Generator().manual_seed(8)
+    n, d, b = 8192, 64, 16
+    q = (torch.randn(1, 240, 16, d, generator=g) / 8).to(torch.bfloat16)
+    k = (torch.randn(1, n, 16, d, generator=g) / 8).to(torch.bfloat16)
+    v = torch.randn(1, n, 16, d, generator=g).to(torch.bfloat16)
+    probe = torch.randn(1, 240, 16, d, generator=g).to(torch.bfloat16)
+    pos = torch.sort(torch.randperm(n, generator=g)[:240]).values[None]
+    _check_dense(q, k, v, pos, probe, b, device, torch.bfloat16, oracle_device=device, label="cfg5")
+
+
+def test_cfg2_full_size(device):
+    """cfg2 at full size: bf16 B1 H8 N=Q=4096 D128 b128, causal; q/k/v ~
+    N(0,1)/sqrt(128), dO ~ N(0,1) (oracle in float32 on the GPU)."""
+    print("dense cfg2", flush=True)
+    q, k, v, pos, do, b = dense_config(CFG2, device=device)
+    _check_dense(q, k, v, pos, do, b, device, torch.bfloat16, oracle_device=device, label="cfg2")
+
+
+def test_native_library_is_the_path(device):
+    """The kernels ran from the in-tree library, bound to torch's HIP runtime."""
+    q = torch.randn(1, 8, 1, 64, device=device)
+    out = dense_attention(q, q, q, torch.arange(8, device=device)[None], 4)
+    torch.cuda.synchronize()
+    assert out.shape == q.shape
+    assert any(r["kernel"] == "dense_fwd" and r["path"] == "hip" for r in launch_report())
+    runtimes = _lib.hip_runtimes_mapped()
+    assert len(runtimes) == 1, runtimes
+    maps = open("/proc/self/maps").read()
+    assert _lib.LIB_PATH in maps
