@@ -1,0 +1,200 @@
+"""Benchmark of the Stack attention operators on one MI355X.
+
+Headline (BASELINE.json metric): dense gated forward+backward TFLOP/s at
+cfg2 (bf16, B1 H8 N=Q=4096 D128 b128, causal), plus the paged sparse top-k
+forward at cfg4 (bf16, B1 H8, 1,048,576 tokens in 128-token pages behind a
+random page table, 16 tail queries, D128 b128, top-64) in GB/s and ms.
+
+A step is one forward+backward (dense) or one forward (sparse) over inputs
+already resident in HBM. Timing: W untimed warmup steps, then K steps
+bracketed by torch.cuda.synchronize(); per-step HIP events (on the stream
+the kernels run on) give the per-step durations. Prints ONE JSON line.
+"""
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "dense fwd+bwd TFLOP/s @N=4096 bf16; sparse fwd GB/s+ms @1M ctx topk=64"
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (AMD published)
+HBM_PEAK_GBS = 8000.0            # MI355X HBM3E
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
+    p.add_argument("--no-sparse", action="store_true", help="skip the cfg4 sparse measurement")
+    p.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU baseline sample")
+    return p.parse_args()
+
+
+def timed_steps(step, warmup, steps, torch):
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    wall0 = time.perf_counter()
+    for begin, end in events:
+        begin.record()
+        step()
+        end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    per = [b.elapsed_time(e) for b, e in events]
+    return per, wall
+
+
+def bench_dense(args, torch, device):
+    from exploration_amd import dense_attention
+    from exploration_amd.workloads import CFG2, dense_config, dense_flops, dense_forward_flops
+
+    q, k, v, pos, do, b = dense_config(CFG2, device=device)
+    q, k, v = (t.requires_grad_() for t in (q, k, v))
+    flops = dense_flops(pos, k.shape[1], q.shape[2], q.shape[3])
+    fwd_flops = dense_forward_flops(pos, k.shape[1], q.shape[2], q.shape[3])
+    phase = {"fwd": [], "bwd": []}
+
+    def step(record=None):
+        q.grad = k.grad = v.grad = None
+        if record is not None:
+            e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+            e0.record()
+        out = dense_attention(q, k, v, pos, b)
+        if record is not None:
+            e1.record()
+        out.backward(do)
+        if record is not None:
+            e2.record()
+            record.append((e0, e1, e2))
+
+    per, wall = timed_steps(step, args.warmup, args.steps, torch)
+    # phase split (separate pass so the headline timing has no extra events)
+    marks = []
+    for _ in range(max(3, args.steps // 2)):
+        step(marks)
+    torch.cuda.synchronize()
+    fwd_ms = statistics.median(a.elapsed_time(b_) for a, b_, _ in marks)
+    bwd_ms = statistics.median(b_.elapsed_time(c) for _, b_, c in marks)
+    ms = sum(per) / len(per)
+    med = statistics.median(per)
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {
+        "ms_mean": ms, "ms_median": med, "ms_min": min(per), "wall_s": wall, "flops": flops,
+        "tflops": tflops, "fwd_ms": fwd_ms, "bwd_ms": bwd_ms,
+        "fwd_tflops": fwd_flops / (fwd_ms * 1e-3) / 1e12,
+        "bwd_tflops": (flops - fwd_flops) / (bwd_ms * 1e-3) / 1e12,
+        "peak_mem_gib": torch.cuda.max_memory_allocated() / 2**30,
+    }
+
+
+def bench_sparse(args, torch, device):
+    from exploration_amd import sparse_attention
+    from exploration_amd.workloads import CFG4, planted_sparse, sparse_bytes
+
+    c = dict(CFG4)
+    q, cache, pos, expected = planted_sparse(**c, device=device)
+    torch.cuda.synchronize()
+    out, sel = sparse_attention(q, cache, pos, c["block"], c["topk"], return_selection=True)
+    exact = bool(torch.equal(sel["indices"], expected))
+    nbytes = sparse_bytes(pos, sel["indices"], c["heads"], c["dim"], c["block"], 2)
+    scan_bytes = c["heads"] * ((c["length"] - 1) // c["block"] - 1) * c["block"] * c["dim"] * 2
+
+    def step():
+        sparse_attention(q, cache, pos, c["block"], c["topk"])
+
+    per, wall = timed_steps(step, args.warmup, args.steps, torch)
+    ms = sum(per) / len(per)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"ms_mean": ms, "ms_median": statistics.median(per), "ms_min": min(per), "wall_s": wall,
+            "bytes": nbytes, "scan_bytes": scan_bytes, "gbs": gbs, "ids_exact": exact}
+
+
+def cpu_baseline(budget_s, torch):
+    """The oracle's eager dense forward+backward (the reference's CPU eager
+    path, st/tools/benchmark.py:27-43) on a bounded sample of cfg2: one of the
+    eight heads, fp32, all host cores."""
+    from exploration_amd.workloads import dense_inputs, dense_flops
+    from oracle import dense as od
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    q, k, v, pos, do = dense_inputs(1, 4096, 4096, 1, 128, torch.float32, seed=0, scale=1 / math.sqrt(128))
+    q, k, v = (t.requires_grad_() for t in (q, k, v))
+    flops = dense_flops(pos, 4096, 1, 128)
+
+    def run():
+        q.grad = k.grad = v.grad = None
+        out = od.eager_attention(q, k, v, pos, 128)
+        out.backward(do)
+
+    t0 = time.perf_counter()
+    run()  # warmup
+    first = time.perf_counter() - t0
+    reps = max(1, min(10, int(budget_s / max(first, 1e-3)) - 1))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": flops / med / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"cfg2 restricted to 1 of 8 heads (B1 H1 N=Q=4096 D128 b128 fp32, causal), "
+                      f"oracle eager forward+backward, median of {reps} after 1 warmup",
+            "seconds_per_step": med}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: multi-GPU paths are out of scope (asked for --gpus {args.gpus})",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    dense = bench_dense(args, torch, device)
+    sparse = None if args.no_sparse else bench_sparse(args, torch, device)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds, torch)
+    line = {
+        "metric": METRIC, "value": round(dense["tflops"], 3), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dense["ms_mean"], 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "cfg2: dense gated attention forward+backward, bf16, B1 H8 N=Q=4096 D128 "
+                               "block 128, causal, q/k/v ~ N(0,1)/sqrt(128), dO ~ N(0,1)",
+                   "global_batch": 1, "seq_len": 4096, "heads": 8, "head_dim": 128, "block_size": 128,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": "dense forward+backward (dense_fwd, dense_bwd_pre, "
+                     "dense_bwd_dq, dense_bwd_dkv)",
+                     "achieved": round(dense["tflops"], 3), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(dense["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "algorithmic_flop": dense["flops"]},
+        "dense": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in dense.items()},
+        "cpu_baseline": cpu,
+    }
+    if sparse is not None:
+        line["sparse"] = {
+            "workload": "cfg4: paged sparse top-k forward, bf16, B1 H8, 1,048,576 tokens in 128-token pages "
+                        "(random page table), 16 tail queries, D128 block 128, top-64, 64 planted blocks/query",
+            "value": round(sparse["gbs"], 2), "unit": "GB/s", "ms": round(sparse["ms_mean"], 4),
+            "ids_bit_exact": sparse["ids_exact"],
+            "roofline": {"bound": "hbm", "achieved": round(sparse["gbs"], 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(sparse["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                         "algorithmic_bytes": sparse["bytes"]},
+            **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in sparse.items()},
+        }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
