@@ -35,7 +35,7 @@ def _digest(src):
     h = hashlib.sha256()
     h.update(" ".join([HIPCC] + FLAGS).encode())
     for name in sorted(os.listdir(CSRC)):
-        if name.endswith((".h", ".hip")):
+        if name.endswith(".h") or name == src:
             with open(os.path.join(CSRC, name), "rb") as f:
                 h.update(name.encode() + f.read())
     with open(os.path.join(INCLUDE, "st_attn.h"), "rb") as f:

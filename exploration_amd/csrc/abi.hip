@@ -150,8 +150,8 @@ int st_dense_bwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_
 static int check_kv(const char* who, int64_t block_size, const void* k, const int32_t* page_table,
                     int64_t page_tokens, int64_t pages_per_seq, int64_t n_tokens, int64_t token_offset) {
   if (!k) return fail(ST_EINVAL, "%s: null key pointer", who);
-  if (n_tokens < 1 || n_tokens > (int64_t(1) << 40))
-    return fail(ST_EINVAL, "%s: n_tokens must be positive", who);
+  if (n_tokens < 1) return fail(ST_EINVAL, "%s: n_tokens must be positive", who);
+  if (n_tokens >= (int64_t(1) << 31)) return fail(ST_EUNSUPPORTED, "%s: n_tokens must be below 2^31", who);
   if (token_offset < 0 || token_offset % block_size != 0)
     return fail(ST_EINVAL, "%s: cache pages/offset must be block aligned", who);
   if (page_table) {

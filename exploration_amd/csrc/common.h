@@ -60,6 +60,22 @@ template <> struct Mma<float> {
   }
 };
 
+// 16x16x32 MFMA (gfx950), 16-bit inputs: lane l holds A[l%16][8*(l/16)+s],
+// B[8*(l/16)+s][l%16] (s = 0..7) and C[4*(l/16)+r][l%16] (r = 0..3).
+template <typename T> struct Mma16;
+template <> struct Mma16<bf16> {
+  typedef bf16x8 Frag;
+  static __device__ __forceinline__ f32x4 mma(Frag a, Frag b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mma16<f16> {
+  typedef f16x8 Frag;
+  static __device__ __forceinline__ f32x4 mma(Frag a, Frag b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
 template <typename T> __device__ __forceinline__ T from_float(float x) { return (T)x; }
 template <typename T> __device__ __forceinline__ float to_float(T x) { return (float)x; }
 
@@ -89,6 +105,18 @@ __device__ __forceinline__ float logaddexp(float a, float b) {
   float m = fmaxf(a, b);
   if (m == kNegInf) return kNegInf;
   return m + __logf(__expf(a - m) + __expf(b - m));
+}
+
+// Asynchronous 16-byte global -> LDS copy (gfx950 global_load_lds): lane l of
+// the wave writes its 16 bytes to lds_base + 16*l, so one instruction fills
+// 1 KiB of LDS in lane order. lds_base must be wave-uniform. Completion is
+// tracked by vmcnt: wait_vm() before the data is read.
+__device__ __forceinline__ void async_copy16(const void* g, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+}
+__device__ __forceinline__ void wait_vm() {
+  __builtin_amdgcn_s_waitcnt(0);
+  __asm__ volatile("" ::: "memory");
 }
 
 // 16-byte global load / store helpers.

@@ -28,9 +28,11 @@ template <typename T, bool PAGED>
 __device__ __forceinline__ const T* kv_token(const KvView& kv, const T* base, int bi, int64_t t, int h,
                                              int H, int D) {
   if constexpr (PAGED) {
-    const int64_t lp = t / kv.page_tokens;
+    // token counts stay below 2^32 (checked by the ABI): 32-bit division
+    const uint32_t pt = (uint32_t)kv.page_tokens;
+    const uint32_t lp = (uint32_t)t / pt;
     const int64_t page = kv.page_table[(int64_t)bi * kv.pages_per_seq + lp];
-    return base + ((page * H + h) * kv.page_tokens + (t - lp * kv.page_tokens)) * D;
+    return base + ((page * H + h) * (int64_t)pt + ((uint32_t)t - lp * pt)) * D;
   } else {
     return base + (((int64_t)bi * kv.n_tokens + t) * H + h) * D;
   }
@@ -143,6 +145,461 @@ __global__ __launch_bounds__(256) void sparse_scores_kernel(SparseArgs a) {
         }
       }
     });
+  }
+}
+
+// Bandwidth-shaped variant for 16-bit KV with head_dim <= 128: each wave
+// copies its 128-key chunk into LDS with coalesced asynchronous 16-byte
+// loads (a 128-token page of one head is one contiguous 32 KiB read), then
+// reads MFMA fragments from an XOR-swizzled layout (chunk c of key row r is
+// stored at chunk c ^ 2*(r % (CPR/2)), so 8 consecutive rows hit distinct
+// banks).
+template <typename T, int DP, bool PAGED, int LOGB_T>
+__global__ __launch_bounds__(64, 2) void sparse_scan_kernel(SparseArgs a) {
+  typedef Mma<T> M;
+  typedef typename M::Frag Frag;
+  static_assert(sizeof(T) == 2 && DP <= 128, "16-bit, head_dim <= 128");
+  constexpr int E = 8;           // elements per 16-byte chunk
+  constexpr int CPR = DP / E;    // chunks per key row
+  constexpr int SWZ = CPR / 2;
+  constexpr int KEYS = 128;
+  constexpr int NST = KEYS / 32;
+  constexpr int NKC = DP / M::KW;
+  constexpr int COPIES = KEYS * CPR / 64;
+  // one wave per workgroup: workgroups on a CU run out of phase, so one
+  // wave's copies overlap another's arithmetic
+  __shared__ __attribute__((aligned(16))) T buf[KEYS * DP];
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 31, half = lane >> 5;
+  const int h = blockIdx.y, bi = blockIdx.z;
+  const int64_t t0 = (int64_t)blockIdx.x * KEYS;
+  const int64_t n_tokens = a.kv.n_tokens;
+  if (t0 >= n_tokens) return;
+  const int b = a.block;
+  const int64_t first_block = t0 / b;
+  const int nblk = KEYS / b;
+  const T* kbase = reinterpret_cast<const T*>(a.kv.k);
+  const T* qbase = reinterpret_cast<const T*>(a.q);
+  bool loaded = false;
+
+  for (int g0 = 0; g0 < a.Q; g0 += 32) {
+    const int row = g0 + col;
+    const bool row_in = row < a.Q;
+    const int64_t p = row_in ? a.pos[(int64_t)bi * a.Q + row] : -1;
+    const int64_t vis_lim = p >= 0 ? p / b - 1 - a.id_base : -1;
+    float any = first_block < vis_lim ? 1.f : 0.f;
+    any = fmaxf(any, other_half(any));
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) any = fmaxf(any, __shfl_xor(any, off, 64));
+
+    Frag qf[NKC];
+    if (any > 0.f) {
+      if (!loaded) {
+        // Row pointers first (page lookups batched, one wait), then the
+        // copies back to back. A chunk inside one page needs one lookup.
+        constexpr int RPI = 64 / CPR;  // key rows per copy instruction
+        const int last = (int)(n_tokens - 1 - t0);  // rows past the range are clamped
+        if (!PAGED || a.kv.page_tokens % KEYS == 0) {
+          const T* base = kv_token<T, PAGED>(a.kv, kbase, bi, t0, h, a.H, a.D);
+          const int64_t stride = kv_stride<PAGED>(a.H, a.D);
+#pragma unroll
+          for (int it = 0; it < COPIES; ++it) {
+            const int slot = it * 64 + lane;
+            const int r = it * RPI + lane / CPR;
+            int chunk = (slot % CPR) ^ (2 * (r % SWZ));
+            if (chunk * E >= a.D) chunk = 0;  // padded columns: any finite data (q pads with zeros)
+            async_copy16(base + (int64_t)(r < last ? r : last) * stride + chunk * E, buf + it * 64 * E);
+          }
+        } else {
+          // pages shorter than the chunk: one lookup per copy (rare path)
+          for (int it = 0; it < COPIES; ++it) {
+            const int slot = it * 64 + lane;
+            const int r = it * RPI + lane / CPR;
+            int chunk = (slot % CPR) ^ (2 * (r % SWZ));
+            if (chunk * E >= a.D) chunk = 0;
+            async_copy16(kv_token<T, PAGED>(a.kv, kbase, bi, t0 + (r < last ? r : last), h, a.H, a.D) + chunk * E,
+                         buf + it * 64 * E);
+          }
+        }
+        loaded = true;
+      }
+      const T* qrow = qbase + (((int64_t)bi * a.Q + (row_in ? row : 0)) * a.H + h) * a.D;
+#pragma unroll
+      for (int c = 0; c < NKC; ++c) {
+        const int d = c * M::KW + half * M::VEC;
+        qf[c] = (row_in && d < a.D) ? *reinterpret_cast<const Frag*>(qrow + d) : Frag{};
+      }
+      wait_vm();
+    }
+    float* out = a.scores + (((int64_t)bi * a.Q + (row_in ? row : 0)) * a.H + h) * a.n_blocks;
+    // One 32-key subtile at a time; blocks wider than a subtile keep a
+    // running (max, sum) across their subtiles.
+    float run_m = kNegInf, run_s = 0.f;
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+      f32x16 acc = zero16();
+      if (any > 0.f) {
+        const int r = 32 * st + col;
+#pragma unroll
+        for (int c = 0; c < NKC; ++c) {
+          const int chunk = (2 * c + half) ^ (2 * (r % SWZ));
+          acc = M::mma(*reinterpret_cast<const Frag*>(buf + r * DP + chunk * E), qf[c], acc);
+        }
+      }
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) {
+        const int64_t tok = t0 + 32 * st + c_row(rr, half);
+        acc[rr] = tok < n_tokens ? acc[rr] * a.scale_log2 : kNegInf;
+      }
+      ([&]<int LOGB>() {
+        auto emit = [&](int bl, float lse2) {
+          if (bl >= nblk || !row_in) return;  // invisible blocks still get -inf
+          const int64_t rel = first_block + bl;
+          if (rel >= a.n_blocks) return;
+          const bool visible = (rel + 1) * b <= n_tokens && rel < vis_lim;
+          out[rel] = visible ? lse2 * kLn2 : kNegInf;
+        };
+        if constexpr (LOGB >= 5) {
+          float m = acc[0];
+#pragma unroll
+          for (int rr = 1; rr < 16; ++rr) m = fmaxf(m, acc[rr]);
+          m = fmaxf(m, other_half(m));
+          float sm = 0.f;
+          if (m != kNegInf) {
+#pragma unroll
+            for (int rr = 0; rr < 16; ++rr) sm += fast_exp2(acc[rr] - m);
+          }
+          sm += other_half(sm);
+          const float nm = fmaxf(run_m, m);
+          if (nm != kNegInf)
+            run_s = (run_m == kNegInf ? 0.f : run_s * fast_exp2(run_m - nm)) +
+                    (m == kNegInf ? 0.f : sm * fast_exp2(m - nm));
+          run_m = nm;
+          constexpr int G = (1 << LOGB) / 32;
+          if ((st + 1) % G == 0) {
+            if (half == 0) emit((32 * st) >> LOGB, run_s > 0.f ? run_m + fast_log2(run_s) : kNegInf);
+            run_m = kNegInf;
+            run_s = 0.f;
+          }
+        } else {
+          f32x16 x[1] = {acc};
+          float mx[1][8], sm[1][8];
+          block_sums<1, LOGB, OpMax>(x, mx);
+#pragma unroll
+          for (int rr = 0; rr < 16; ++rr) {
+            const float m = mx[0][blk_slot<LOGB>(rr)];
+            x[0][rr] = m == kNegInf ? 0.f : fast_exp2(x[0][rr] - m);
+          }
+          block_sums<1, LOGB, OpAdd>(x, sm);
+          if (!BlkSlots<LOGB>::per_half && half != 0) return;
+#pragma unroll
+          for (int j = 0; j < BlkSlots<LOGB>::n; ++j)
+            emit(blk_index<LOGB>(st, j, half), sm[0][j] > 0.f ? mx[0][j] + fast_log2(sm[0][j]) : kNegInf);
+        }
+      }).template operator()<LOGB_T>();
+    }
+  }
+  if (loaded) wait_vm();  // no copy may still target LDS when the wave ends
+}
+
+// ---------------------------------------------------------------------------
+// Direct variant for 16-bit KV, head_dim a multiple of 32 and <= 128:
+// v_mfma_f32_16x16x32 with S^T = K Q^T for 16 queries at a time. Lane l
+// loads 16 bytes of key row l%16 at dims 32c + 8*(l/16), so the four lanes
+// of a key read 64 contiguous bytes per instruction, straight into
+// registers: the bytes in flight are bounded by registers, not by LDS. A
+// score row lives in lanes j, j+16, j+32, j+48 (4 keys each per 16-key
+// subtile); block reductions are in-lane plus two cross-lane steps.
+template <typename T, int DP, bool PAGED, int LOGB>
+__global__ __launch_bounds__(256, 2) void sparse_scan16_kernel(SparseArgs a) {
+  typedef Mma16<T> M;
+  typedef typename M::Frag Frag;
+  constexpr int KEYS = 128;             // keys per wave
+  constexpr int NS = KEYS / 16;         // 16-key subtiles
+  constexpr int NKC = DP / 32;          // contraction chunks
+  constexpr int B = 1 << LOGB;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int h = blockIdx.y, bi = blockIdx.z;
+  const int64_t t0 = ((int64_t)blockIdx.x * 4 + wave) * KEYS;
+  const int64_t n_tokens = a.kv.n_tokens;
+  if (t0 >= n_tokens) return;
+  const int64_t first_block = t0 >> LOGB;
+  const T* kbase = reinterpret_cast<const T*>(a.kv.k);
+  const T* qbase = reinterpret_cast<const T*>(a.q);
+  const int64_t stride = kv_stride<PAGED>(a.H, a.D);
+  const int last = (int)(n_tokens - 1 - t0);
+  // key row pointers of this lane's 8 subtiles (one page lookup per chunk
+  // when pages hold whole chunks)
+  const T* krow[NS];
+  if (!PAGED || a.kv.page_tokens % KEYS == 0) {
+    const T* base = kv_token<T, PAGED>(a.kv, kbase, bi, t0, h, a.H, a.D);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int r = 16 * s + j;
+      krow[s] = base + (int64_t)(r < last ? r : last) * stride;
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int r = 16 * s + j;
+      krow[s] = kv_token<T, PAGED>(a.kv, kbase, bi, t0 + (r < last ? r : last), h, a.H, a.D);
+    }
+  }
+  bool loaded = false;
+  Frag kf[NS][NKC];
+  for (int g0 = 0; g0 < a.Q; g0 += 16) {
+    const int row = g0 + j;
+    const bool row_in = row < a.Q;
+    const int64_t p = row_in ? a.pos[(int64_t)bi * a.Q + row] : -1;
+    const int64_t vis_lim = p >= 0 ? p / (int64_t)B - 1 - a.id_base : -1;
+    float any = first_block < vis_lim ? 1.f : 0.f;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) any = fmaxf(any, __shfl_xor(any, off, 64));
+    float* out = a.scores + (((int64_t)bi * a.Q + (row_in ? row : 0)) * a.H + h) * a.n_blocks;
+    f32x4 acc[NS];
+    if (any > 0.f) {
+      if (!loaded) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+          for (int c = 0; c < NKC; ++c) {
+            const int d = 32 * c + 8 * g;
+            kf[s][c] = d < a.D ? *reinterpret_cast<const Frag*>(krow[s] + d) : Frag{};
+          }
+        loaded = true;
+      }
+      Frag qf[NKC];
+      const T* qrow = qbase + (((int64_t)bi * a.Q + (row_in ? row : 0)) * a.H + h) * a.D;
+#pragma unroll
+      for (int c = 0; c < NKC; ++c) {
+        const int d = 32 * c + 8 * g;
+        qf[c] = (row_in && d < a.D) ? *reinterpret_cast<const Frag*>(qrow + d) : Frag{};
+      }
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        f32x4 c4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NKC; ++c) c4 = M::mma(kf[s][c], qf[c], c4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t tok = t0 + 16 * s + 4 * g + r;
+          c4[r] = tok < n_tokens ? c4[r] * a.scale_log2 : kNegInf;
+        }
+        acc[s] = c4;
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) acc[s] = f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
+    }
+    if (!row_in) continue;
+    auto emit = [&](int bl, float lse2) {
+      const int64_t rel = first_block + bl;
+      if (rel >= a.n_blocks) return;
+      const bool visible = (rel + 1) * B <= n_tokens && rel < vis_lim;
+      out[rel] = visible ? lse2 * kLn2 : kNegInf;
+    };
+    if constexpr (B >= 16) {
+      // a block = B/16 whole subtiles; lanes g hold 4 keys of each
+      constexpr int SPB = B / 16;
+#pragma unroll
+      for (int b0 = 0; b0 < NS; b0 += SPB) {
+        float m = kNegInf;
+#pragma unroll
+        for (int s = b0; s < b0 + SPB; ++s)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) m = fmaxf(m, acc[s][r]);
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        float sm = 0.f;
+        if (m != kNegInf) {
+#pragma unroll
+          for (int s = b0; s < b0 + SPB; ++s)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sm += fast_exp2(acc[s][r] - m);
+        }
+        sm += __shfl_xor(sm, 16, 64);
+        sm += __shfl_xor(sm, 32, 64);
+        if (g == 0) emit(b0 / SPB, sm > 0.f ? m + fast_log2(sm) : kNegInf);
+      }
+    } else if constexpr (B == 8) {
+      // keys 8k..8k+7 of a subtile live in lane groups g = 2k, 2k+1
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        float m = fmaxf(fmaxf(acc[s][0], acc[s][1]), fmaxf(acc[s][2], acc[s][3]));
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        float sm = 0.f;
+        if (m != kNegInf)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sm += fast_exp2(acc[s][r] - m);
+        sm += __shfl_xor(sm, 16, 64);
+        if ((g & 1) == 0) emit(2 * s + (g >> 1), sm > 0.f ? m + fast_log2(sm) : kNegInf);
+      }
+    } else {
+      // blocks of 4 (one lane group) or 2 (half of one)
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int q0 = 0; q0 < 4; q0 += B) {
+          float m = acc[s][q0];
+#pragma unroll
+          for (int r = 1; r < B; ++r) m = fmaxf(m, acc[s][q0 + r]);
+          float sm = 0.f;
+          if (m != kNegInf)
+#pragma unroll
+            for (int r = 0; r < B; ++r) sm += fast_exp2(acc[s][q0 + r] - m);
+          emit((16 * s + 4 * g + q0) >> LOGB, sm > 0.f ? m + fast_log2(sm) : kNegInf);
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Single-pass top-k for k <= 64: each wave streams a quarter of the row,
+// keeps its running top-64 as one 64-bit key per lane (sorted descending
+// across lanes), and only keys above the current 64th key are buffered and
+// merged (bitonic sort of 64 + bitonic merge). The four wave lists are then
+// merged by wave 0. Exact: keys are distinct (score bits, ~block id).
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t x, int m) {
+  const int lo = __shfl_xor((int)(uint32_t)x, m, 64);
+  const int hi = __shfl_xor((int)(uint32_t)(x >> 32), m, 64);
+  return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+
+__device__ __forceinline__ uint64_t wave_sort_asc(uint64_t x, int lane) {
+#pragma unroll
+  for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const uint64_t y = shfl_xor64(x, j);
+      const bool keep_min = ((lane & j) == 0) == ((lane & k) == 0);
+      x = keep_min ? (x < y ? x : y) : (x > y ? x : y);
+    }
+  return x;
+}
+
+// r sorted descending, c sorted ascending: the top 64 of both, descending.
+__device__ __forceinline__ uint64_t wave_merge_desc(uint64_t r, uint64_t c, int lane) {
+  uint64_t x = r > c ? r : c;
+#pragma unroll
+  for (int j = 32; j > 0; j >>= 1) {
+    const uint64_t y = shfl_xor64(x, j);
+    x = ((lane & j) == 0) ? (x > y ? x : y) : (x < y ? x : y);
+  }
+  return x;
+}
+
+__device__ __forceinline__ uint64_t lane63(uint64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)x, 63);
+  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint32_t ordered_bits(float x);
+
+__global__ __launch_bounds__(256) void sparse_select64_kernel(int64_t n_blocks, int topk, int64_t id_base,
+                                                              const float* scores, int64_t* ids, float* top,
+                                                              float* log_zr) {
+  __shared__ uint64_t cand[4][128];
+  __shared__ uint64_t lists[4][64];
+  __shared__ float red_m[4], red_s[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t row = blockIdx.x;
+  const float* s = scores + row * n_blocks;
+  const int64_t seg = (((n_blocks + 3) / 4) + 63) / 64 * 64;
+  const int64_t lo = wave * seg;
+  const int64_t hi = lo + seg < n_blocks ? lo + seg : n_blocks;
+  float m = kNegInf, sum = 0.f;
+  uint64_t best = 0, theta = 0;
+  int cnt = 0;
+  auto flush = [&](int take) {
+    uint64_t x = lane < take ? cand[wave][lane] : 0;
+    x = wave_sort_asc(x, lane);
+    best = wave_merge_desc(best, x, lane);
+    theta = lane63(best);
+  };
+  // Batches of 32 scores per lane. Each batch first merges the 64 lane
+  // maxima (64 distinct keys, so the 64th best key of the batch is at least
+  // their minimum); afterwards only keys above the running 64th key are
+  // buffered and merged.
+  constexpr int BATCH = 32;
+  auto key_at = [&](float x, int64_t i) -> uint64_t {
+    return ((uint64_t)ordered_bits(x) << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+  };
+  for (int64_t base0 = lo; base0 < hi; base0 += 64 * BATCH) {
+    float xs[BATCH];
+#pragma unroll
+    for (int q = 0; q < BATCH; ++q) {
+      const int64_t i = base0 + 64 * q + lane;
+      xs[q] = i < hi ? s[i] : kNegInf;
+    }
+    uint64_t kmax = 0;
+#pragma unroll
+    for (int q = 0; q < BATCH; ++q) {
+      const int64_t i = base0 + 64 * q + lane;
+      const float x = xs[q];
+      if (x > m) {
+        sum = (m == kNegInf ? 0.f : sum * __expf(m - x)) + 1.f;
+        m = x;
+      } else if (x != kNegInf) {
+        sum += __expf(x - m);
+      }
+      const uint64_t key = i < hi ? key_at(x, i) : 0;
+      kmax = key > kmax ? key : kmax;
+    }
+    best = wave_merge_desc(best, wave_sort_asc(kmax, lane), lane);
+    theta = lane63(best);
+#pragma unroll
+    for (int q = 0; q < BATCH; ++q) {
+      const int64_t i = base0 + 64 * q + lane;
+      const uint64_t key = i < hi ? key_at(xs[q], i) : 0;
+      const bool pass = key > theta && key != kmax;
+      const uint64_t mask = __ballot(pass);
+      if (mask == 0) continue;
+      const int rank = __popcll(mask & ((1ull << lane) - 1ull));
+      if (pass) cand[wave][cnt + rank] = key;
+      cnt += __popcll(mask);
+      if (cnt >= 64) {
+        flush(64);
+        const int rest = cnt - 64;
+        uint64_t moved = lane < rest ? cand[wave][64 + lane] : 0;
+        if (lane < rest) cand[wave][lane] = moved;
+        cnt = rest;
+      }
+    }
+  }
+  if (cnt > 0) flush(cnt);
+  lists[wave][lane] = best;
+  // per-wave logsumexp partial
+  float mw = m;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mw = fmaxf(mw, __shfl_xor(mw, off, 64));
+  float sw = (m == kNegInf) ? 0.f : sum * __expf(m - mw);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) sw += __shfl_xor(sw, off, 64);
+  if (lane == 0) { red_m[wave] = mw; red_s[wave] = sw; }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 1; w < 4; ++w) best = wave_merge_desc(best, lists[w][63 - lane], lane);
+  if (lane < topk) {
+    float sc = kNegInf;
+    int64_t id = -1;
+    if (best != 0) {
+      const uint32_t ob = (uint32_t)(best >> 32);
+      const uint32_t u = (ob & 0x80000000u) ? (ob & 0x7fffffffu) : ~ob;
+      sc = __uint_as_float(u);
+      if (sc != kNegInf) id = (int64_t)(0xffffffffu - (uint32_t)(best & 0xffffffffu)) + id_base;
+    }
+    top[row * topk + lane] = sc;
+    ids[row * topk + lane] = id;
+  }
+  if (lane == 0) {
+    const float mm = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+    float tot = 0.f;
+    if (mm != kNegInf)
+      for (int w = 0; w < 4; ++w) tot += red_m[w] == kNegInf ? 0.f : red_s[w] * __expf(red_m[w] - mm);
+    log_zr[row] = (mm == kNegInf || !(tot > 0.f)) ? kNegInf : mm + __logf(tot);
   }
 }
 
@@ -319,14 +776,26 @@ __global__ __launch_bounds__(256) void sparse_pop_kernel(SparseArgs a) {
     const T* kb = kv_token<T, PAGED>(a.kv, reinterpret_cast<const T*>(a.kv.k), bi, tstart, h, a.H, a.D);
     const T* vb = kv_token<T, PAGED>(a.kv, reinterpret_cast<const T*>(a.kv.v), bi, tstart, h, a.H, a.D);
     const int ntok = (int)(hi - lo);  // tokens from tstart on (lo == tstart + token_offset)
-    for (int i0 = 0; i0 < ntok; i0 += TPI) {
+    constexpr int BATCH = 8;  // token rounds whose loads are in flight together
+    for (int i00 = 0; i00 < ntok; i00 += TPI * BATCH) {
+     V kvs[BATCH], vvs[BATCH];
+#pragma unroll
+     for (int j = 0; j < BATCH; ++j) {
+       const int i = i00 + TPI * j + g;
+       kvs[j] = V{};
+       vvs[j] = V{};
+       if (i < ntok && e0 < a.D) {
+         kvs[j] = load_vec<V>(kb + (int64_t)i * stride + e0);
+         vvs[j] = load_vec<V>(vb + (int64_t)i * stride + e0);
+       }
+     }
+#pragma unroll
+     for (int j = 0; j < BATCH; ++j) {
+      const int i0 = i00 + TPI * j;
+      if (i0 >= ntok) break;
       const int i = i0 + g;
       const bool valid = i < ntok;
-      V kv = {}, vv = {};
-      if (valid && e0 < a.D) {
-        kv = load_vec<V>(kb + (int64_t)i * stride + e0);
-        vv = load_vec<V>(vb + (int64_t)i * stride + e0);
-      }
+      const V kv = kvs[j], vv = vvs[j];
       float dot = 0.f;
 #pragma unroll
       for (int e = 0; e < E; ++e) dot += q[e] * to_float<T>(kv[e]);
@@ -342,6 +811,7 @@ __global__ __launch_bounds__(256) void sparse_pop_kernel(SparseArgs a) {
         for (int e = 0; e < E; ++e) o[e] = o[e] * alpha + pw * to_float<T>(vv[e]);
         m = mn;
       }
+     }
     }
   }
   // merge the TPI token groups (lanes e0-aligned, differing in g)
@@ -414,8 +884,41 @@ template <typename T, int DP>
 static hipError_t scores_dp(const SparseArgs& a, hipStream_t s) {
   const int64_t chunks = (a.kv.n_tokens + 127) / 128;
   dim3 grid((unsigned)((chunks + 3) / 4), a.H, a.B);
-  if (a.kv.page_table) hipLaunchKernelGGL((sparse_scores_kernel<T, DP, true>), grid, dim3(256), 0, s, a);
-  else hipLaunchKernelGGL((sparse_scores_kernel<T, DP, false>), grid, dim3(256), 0, s, a);
+  if constexpr (sizeof(T) == 2 && DP <= 128) {
+    if (a.D % 32 == 0) {
+      auto go16 = [&]<int LOGB>() {
+        if (a.kv.page_table) hipLaunchKernelGGL((sparse_scan16_kernel<T, DP, true, LOGB>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((sparse_scan16_kernel<T, DP, false, LOGB>), grid, dim3(256), 0, s, a);
+      };
+      switch (a.logb) {
+        case 1: go16.template operator()<1>(); break;
+        case 2: go16.template operator()<2>(); break;
+        case 3: go16.template operator()<3>(); break;
+        case 4: go16.template operator()<4>(); break;
+        case 5: go16.template operator()<5>(); break;
+        case 6: go16.template operator()<6>(); break;
+        default: go16.template operator()<7>(); break;
+      }
+      return hipGetLastError();
+    }
+    dim3 g1((unsigned)chunks, a.H, a.B);
+    auto go = [&]<int LOGB>() {
+      if (a.kv.page_table) hipLaunchKernelGGL((sparse_scan_kernel<T, DP, true, LOGB>), g1, dim3(64), 0, s, a);
+      else hipLaunchKernelGGL((sparse_scan_kernel<T, DP, false, LOGB>), g1, dim3(64), 0, s, a);
+    };
+    switch (a.logb) {
+      case 1: go.template operator()<1>(); break;
+      case 2: go.template operator()<2>(); break;
+      case 3: go.template operator()<3>(); break;
+      case 4: go.template operator()<4>(); break;
+      case 5: go.template operator()<5>(); break;
+      case 6: go.template operator()<6>(); break;
+      default: go.template operator()<7>(); break;
+    }
+  } else {
+    if (a.kv.page_table) hipLaunchKernelGGL((sparse_scores_kernel<T, DP, true>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((sparse_scores_kernel<T, DP, false>), grid, dim3(256), 0, s, a);
+  }
   return hipGetLastError();
 }
 
@@ -437,8 +940,12 @@ hipError_t launch_sparse_scores(int dtype, const SparseArgs& a, hipStream_t stre
 hipError_t launch_sparse_select(int64_t rows, int64_t n_blocks, int topk, int64_t id_base,
                                 const float* scores, int64_t* ids, float* top, float* log_zr,
                                 hipStream_t stream) {
-  hipLaunchKernelGGL(sparse_select_kernel, dim3((unsigned)rows), dim3(256), 0, stream, n_blocks, topk, id_base,
-                     scores, ids, top, log_zr);
+  if (topk <= 64)
+    hipLaunchKernelGGL(sparse_select64_kernel, dim3((unsigned)rows), dim3(256), 0, stream, n_blocks, topk, id_base,
+                       scores, ids, top, log_zr);
+  else
+    hipLaunchKernelGGL(sparse_select_kernel, dim3((unsigned)rows), dim3(256), 0, stream, n_blocks, topk, id_base,
+                       scores, ids, top, log_zr);
   return hipGetLastError();
 }
 
