@@ -33,6 +33,9 @@ struct DenseArgs {
 // Each returns hipSuccess or the launch error; the arguments were validated
 // by the caller (dtype, head_dim <= 256, block a power of two in [2,128]).
 hipError_t launch_dense_fwd(int dtype, const DenseArgs& a, hipStream_t stream);
+// Pipelined forward for 16-bit inputs with head_dim 64 or 128.
+bool dense_fwd_fast_supported(int dtype, const DenseArgs& a);
+hipError_t launch_dense_fwd_fast(int dtype, const DenseArgs& a, hipStream_t stream);
 hipError_t launch_dense_bwd(int dtype, const DenseArgs& a, hipStream_t stream);
 
 }  // namespace st

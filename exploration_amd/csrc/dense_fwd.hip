@@ -265,6 +265,7 @@ static hipError_t launch_fwd_t(const DenseArgs& a, hipStream_t stream) {
 }
 
 hipError_t launch_dense_fwd(int dtype, const DenseArgs& a, hipStream_t stream) {
+  if (dense_fwd_fast_supported(dtype, a)) return launch_dense_fwd_fast(dtype, a, stream);
   switch (dtype) {
     case kBF16: return launch_fwd_t<bf16>(a, stream);
     case kF16: return launch_fwd_t<f16>(a, stream);

@@ -222,6 +222,78 @@ template <int LOGB> struct BlkSlots {
   static constexpr bool per_half = LOGB <= 2;
 };
 
+// ---------------------------------------------------------------------------
+// Asynchronously staged, XOR-swizzled row-major tiles (16-bit types).
+// A tile row of DP elements is CPR = DP/8 chunks of 16 bytes; logical chunk c
+// of row r is stored at chunk c ^ swz(r), swz(r) = 2*(r % (CPR/2)). Then
+//  * 8 consecutive rows read at one logical chunk (ds_read_b128 fragments)
+//    hit 8 distinct 16-byte bank groups, and
+//  * 4 consecutive rows read 32 logical bytes each (ds_read_tr16_b64
+//    fragments) hit 4 distinct 32-byte bank groups.
+template <int DP> __device__ __forceinline__ int swz(int r) { return 2 * (r % (DP / 16)); }
+
+// Issue the asynchronous copies of rows [r0, r0+ROWS) x [0, DP) of a
+// [*, stride] matrix into a swizzled LDS tile; rows >= nrows re-read row
+// nrows-1 and chunks at or beyond ncols re-read chunk 0 (finite data whose
+// products are masked or discarded). Every wave of the workgroup takes part.
+template <typename T, int ROWS, int DP, int NWAVES>
+__device__ __forceinline__ void stage_async(T* lds, const T* g, int64_t stride, int r0, int nrows,
+                                            int ncols) {
+  static_assert(sizeof(T) == 2, "16-bit tiles");
+  constexpr int CPR = DP / 8;
+  constexpr int SLOTS = ROWS * CPR;
+  static_assert(SLOTS % (64 * NWAVES) == 0, "tile must split evenly over the waves");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int it = 0; it < SLOTS / (64 * NWAVES); ++it) {
+    const int base = (it * NWAVES + wave) * 64;
+    const int p = base + lane;
+    const int r = p / CPR;
+    int c = (p % CPR) ^ swz<DP>(r);
+    if (c * 8 >= ncols) c = 0;
+    int row = r0 + r;
+    row = row < nrows ? row : nrows - 1;
+    async_copy16(g + (int64_t)row * stride + c * 8, lds + base * 8);
+  }
+}
+
+// MFMA fragment (8 elements) of swizzled row n, logical chunk c.
+template <typename T, int DP>
+__device__ __forceinline__ typename Mma<T>::Frag frag_swz(const T* lds, int n, int c) {
+  return *reinterpret_cast<const typename Mma<T>::Frag*>(lds + n * DP + ((c ^ swz<DP>(n)) * 8));
+}
+
+// Transposed MFMA fragment from a swizzled row-major tile X[key][d]: the A
+// operand of acc^T[d][row] += X^T P^T for dims [d0, d0+32) and the 16 keys
+// [k0, k0+16), in the permuted key order of frag_from_c (slots 0..3 <->
+// k0+4h+{0..3}, slots 4..7 <-> k0+8+4h+{0..3}). Two ds_read_tr16_b64: within
+// each 16-lane group, out[i][j] = in[4j + i/4][i%4] where in[s] is the 8
+// bytes lane s reads, so lane s reads row k+s/4, dims d+4(s%4)..+3.
+template <typename T, int DP>
+__device__ __forceinline__ typename Mma<T>::Frag frag_tr(const T* lds, int k0, int d0, int lane) {
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  const int gi = lane >> 4, s = lane & 15;
+  const int half = gi >> 1;
+  const int d = d0 + 16 * (gi & 1) + 4 * (s & 3);
+  const int row0 = k0 + 4 * half + (s >> 2);
+  const int row1 = row0 + 8;
+  const int lc = d >> 3, off = d & 7;
+  const T* p0 = lds + row0 * DP + ((lc ^ swz<DP>(row0)) * 8) + off;
+  const T* p1 = lds + row1 * DP + ((lc ^ swz<DP>(row1)) * 8) + off;
+  s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)p0);
+  s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)p1);
+  typedef short s8 __attribute__((ext_vector_type(8)));
+  s8 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(typename Mma<T>::Frag, v);
+}
+
+// Half-wave exchange on gfx950 without the LDS crossbar: returns x of the
+// lane 32 positions away.
+__device__ __forceinline__ float swap_halves(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
 // Runs body.template operator()<LOGB>() for the runtime block size.
 template <typename F> __device__ __forceinline__ void dispatch_logb(int logb, F&& body) {
   switch (logb) {
