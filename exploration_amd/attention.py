@@ -92,9 +92,9 @@ class _DenseHip(torch.autograd.Function):
         batch, queries, heads, dim = q.shape
         keys = k.shape[1]
         dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-        ws_bytes = lib.st_dense_bwd_workspace_bytes(batch, queries, heads)
-        ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
         code = _lib.DTYPE_CODES[q.dtype]
+        ws_bytes = lib.st_dense_bwd_workspace_bytes(code, batch, queries, keys, heads, dim, ctx.block_size)
+        ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
         _lib.check(lib.st_dense_bwd(code, batch, queries, keys, heads, dim, ctx.block_size,
                                     _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(positions),
                                     _lib.ptr(out), _lib.ptr(rc), _lib.ptr(pr), _lib.ptr(zr), _lib.ptr(z),

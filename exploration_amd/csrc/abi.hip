@@ -108,8 +108,12 @@ int st_dense_fwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_
   return launched(st::launch_dense_fwd(dtype, a, as_stream(stream)), "st_dense_fwd");
 }
 
-size_t st_dense_bwd_workspace_bytes(int64_t batch, int64_t queries, int64_t heads) {
-  return 2 * align256(sizeof(float) * (size_t)batch * queries * heads);
+size_t st_dense_bwd_workspace_bytes(int dtype, int64_t batch, int64_t queries, int64_t keys,
+                                    int64_t heads, int64_t head_dim, int64_t block_size) {
+  if (check_dtype(dtype) || check_sizes(batch, queries, keys, heads, head_dim, block_size) ||
+      check_envelope(head_dim, block_size))
+    return 0;
+  return st::dense_bwd_plan(dtype, batch, queries, keys, heads, head_dim, block_size).total;
 }
 
 int st_dense_bwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_t heads,
@@ -124,7 +128,8 @@ int st_dense_bwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_
   if (!q || !k || !v || !positions || !out || !rc || !pr || !zr || !z || !dout || !dq || !dk || !dv ||
       !workspace)
     return fail(ST_EINVAL, "st_dense_bwd: null pointer argument");
-  const size_t need = st_dense_bwd_workspace_bytes(batch, queries, heads);
+  const st::DenseBwdPlan plan = st::dense_bwd_plan(dtype, batch, queries, keys, heads, head_dim, block_size);
+  const size_t need = plan.total;
   if (workspace_bytes < need)
     return fail(ST_EINVAL, "st_dense_bwd: workspace of %zu bytes, %zu needed", workspace_bytes, need);
   if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
@@ -134,8 +139,17 @@ int st_dense_bwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_
   a.out = const_cast<void*>(out);
   a.rc = const_cast<float*>(rc); a.pr = const_cast<float*>(pr);
   a.zr = const_cast<float*>(zr); a.z = const_cast<float*>(z);
-  a.delta = reinterpret_cast<float*>(workspace);
-  a.rho = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + need / 2);
+  char* ws = reinterpret_cast<char*>(workspace);
+  a.delta = reinterpret_cast<float*>(ws);
+  a.rho = reinterpret_cast<float*>(ws + plan.off_rho);
+  if (plan.fast) {
+    a.lim = reinterpret_cast<int*>(ws + plan.off_lim);
+    a.tmin = reinterpret_cast<int*>(ws + plan.off_tmin);
+    a.tmax = reinterpret_cast<int*>(ws + plan.off_tmax);
+    a.tab = reinterpret_cast<float2*>(ws + plan.off_tab);
+    a.Qp = plan.Qp;
+    a.nblk = plan.nblk;
+  }
   a.dq = dq; a.dk = dk; a.dv = dv;
   a.B = (int)batch; a.Q = (int)queries; a.N = (int)keys; a.H = (int)heads; a.D = (int)head_dim;
   a.block = (int)block_size; a.logb = log2i(block_size);

@@ -89,8 +89,12 @@ __device__ __forceinline__ f32x16 zero16() {
 // Row (within a 32x32 C tile) of accumulator register r in a lane of half h.
 __device__ __forceinline__ int c_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
 
-// Value held by the lane 32 positions away (the other half of the wave).
-__device__ __forceinline__ float other_half(float x) { return __shfl_xor(x, 32, 64); }
+// Value held by the lane 32 positions away (the other half of the wave), via
+// gfx950's v_permlane32_swap rather than the LDS crossbar.
+__device__ __forceinline__ float other_half(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }

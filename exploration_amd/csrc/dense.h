@@ -24,8 +24,14 @@ struct DenseArgs {
   void* dq;               // [B,Q,H,D]
   void* dk;               // [B,N,H,D]
   void* dv;               // [B,N,H,D]
+  // pipelined backward workspace (null when the generic backward runs)
+  int* lim;               // [B,Qp] last visible key of a row, -1 = none
+  int* tmin;              // [B,Qp/64] min of lim over 64-row tiles
+  int* tmax;              // [B,Qp/64] max of lim over 64-row tiles
+  float2* tab;            // [B*H, nblk, Qp] per (key block, row): (beta, eps)
   int B, Q, N, H, D;
   int block, logb;
+  int Qp, nblk;           // Q rounded up to 64; key blocks in whole 128-key tiles
   float scale;            // 1/sqrt(D)
   float scale_log2;       // log2(e)/sqrt(D)
 };
@@ -37,5 +43,17 @@ hipError_t launch_dense_fwd(int dtype, const DenseArgs& a, hipStream_t stream);
 bool dense_fwd_fast_supported(int dtype, const DenseArgs& a);
 hipError_t launch_dense_fwd_fast(int dtype, const DenseArgs& a, hipStream_t stream);
 hipError_t launch_dense_bwd(int dtype, const DenseArgs& a, hipStream_t stream);
+
+// Workspace of the backward: delta and rho for every path, plus the row
+// limits, row-tile statistics and (beta, eps) table of the pipelined path
+// when it applies (16-bit, head_dim 64/128, table within its size cap).
+struct DenseBwdPlan {
+  bool fast;
+  int Qp, nblk, n_rtiles;
+  size_t off_rho, off_lim, off_tmin, off_tmax, off_tab, total;
+};
+DenseBwdPlan dense_bwd_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t H, int64_t D,
+                            int64_t block);
+hipError_t launch_dense_bwd_fast(int dtype, const DenseArgs& a, hipStream_t stream);
 
 }  // namespace st

@@ -1,0 +1,599 @@
+// Gated dense block attention, backward: pipelined gfx950 path for 16-bit
+// inputs with head_dim 64 or 128 (the hot shapes).
+//
+// Derivative (st/ops/kernels/dense.py:89-182; st/ops/attention.py:105-139):
+// for a query row with statistics Z, log Z_R, delta = dO.O, rho = dO.RC -
+// delta*PR and logits a_i = q.k_i/sqrt(D),
+//   remote key i in block j: u_i = exp(a_i - log Z_R), U_j = sum_{i in j} u_i,
+//     P_i = u_i U_j e^{log Z_R - Z},
+//     dA_i = P_i (dP_i - delta) + u_i (G_j / U_j - rho),
+//     G_j = sum_{i in j} P_i (dP_i - delta);
+//   local key i: P_i = exp(a_i - Z), dA_i = P_i (dP_i - delta).
+// Both cases have the form
+//   P_i = exp2(a_i log2(e) - beta_j),  dA_i = P_i (dP_i + eps_j)
+// with one (beta_j, eps_j) per (row, key block):
+//   remote: beta_j = Z log2(e) - log2 U_j,
+//           eps_j = (G_j / U_j - rho) / (U_j e^{log Z_R - Z}) - delta;
+//   local:  beta_j = Z log2(e), eps_j = -delta;
+//   beyond the row's window: beta_j = +inf (P = 0), eps_j = 0.
+//
+// Kernels:
+//  * dense_bwd_rows: per row the last visible key, per 64-row tile its
+//    min/max (which row tiles a key tile must visit, and which need masks);
+//  * dense_bwd_dq_fast: lane = query row, the layout in which block sums are
+//    in-lane; recomputes S and dP, writes dQ and the (beta, eps) table;
+//  * dense_bwd_dkv_fast: lane = key; per element one exp2 and two FMAs from
+//    the table, no cross-lane or cross-wave reductions, dK/dV in registers.
+// K/V (dQ kernel) and Q/dO (dK/dV kernel) tiles are staged with asynchronous
+// global->LDS copies into swizzled, double-buffered LDS; transposed operands
+// come from ds_read_tr16_b64. Workgroups are numbered head-fastest, so the
+// dispatcher's round-robin over the XCDs keeps one head per XCD L2.
+#include "dense.h"
+#include "tile.h"
+
+namespace st {
+
+namespace {
+
+constexpr int kKT = 128;       // keys per dK/dV workgroup and per dQ key tile
+constexpr int kRT = 64;        // query rows per dK/dV step / row-tile statistic
+constexpr int kMaxRTiles = 2048;
+constexpr size_t kMaxTable = size_t(4) << 30;
+constexpr float kInf = __builtin_inff();
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+}  // namespace
+
+DenseBwdPlan dense_bwd_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t H, int64_t D,
+                            int64_t block) {
+  DenseBwdPlan p = {};
+  const size_t rows = align256(sizeof(float) * (size_t)(B * Q * H));
+  p.off_rho = rows;
+  p.total = 2 * rows;
+  const bool shape_ok = (dtype == kBF16 || dtype == kF16) && (D == 64 || D == 128) && block <= kKT;
+  if (!shape_ok) return p;
+  const int64_t Qp = (Q + kRT - 1) / kRT * kRT;
+  const int64_t n_rtiles = Qp / kRT;
+  const int64_t nblk = (N + kKT - 1) / kKT * (kKT / block);
+  const size_t tab = sizeof(float2) * (size_t)(B * H) * (size_t)nblk * (size_t)Qp;
+  if (n_rtiles > kMaxRTiles || tab > kMaxTable) return p;
+  p.fast = true;
+  p.Qp = (int)Qp;
+  p.nblk = (int)nblk;
+  p.n_rtiles = (int)n_rtiles;
+  p.off_lim = p.total;
+  p.off_tmin = p.off_lim + align256(sizeof(int) * (size_t)(B * Qp));
+  p.off_tmax = p.off_tmin + align256(sizeof(int) * (size_t)(B * n_rtiles));
+  p.off_tab = p.off_tmax + align256(sizeof(int) * (size_t)(B * n_rtiles));
+  p.total = p.off_tab + align256(tab);
+  return p;
+}
+
+// ---------------------------------------------------------------------------
+// Per row: the last visible key (min(p, N-1); -1 for padding rows and rows
+// beyond Q); per 64-row tile (one wave) its min and max.
+__global__ __launch_bounds__(256) void dense_bwd_rows_kernel(DenseArgs a) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  // B*Qp is a multiple of 64: whole waves leave together
+  if (idx >= (int64_t)a.B * a.Qp) return;
+  const int bi = (int)(idx / a.Qp), row = (int)(idx % a.Qp);
+  int lim = -1;
+  if (row < a.Q) {
+    const int64_t p = a.pos[(int64_t)bi * a.Q + row];
+    if (p >= 0) lim = (int)(p < a.N - 1 ? p : a.N - 1);
+  }
+  a.lim[idx] = lim;
+  int mx = lim, mn = lim;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    mx = max(mx, __shfl_xor(mx, off, 64));
+    mn = min(mn, __shfl_xor(mn, off, 64));
+  }
+  if ((threadIdx.x & 63) == 0) {
+    a.tmax[idx / kRT] = mx;
+    a.tmin[idx / kRT] = mn;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dQ and the (beta, eps) table. A workgroup owns 128 query rows (wave w: rows
+// 32w..32w+31, lane = row) of one (batch, head) and walks the key tiles of
+// its causal range. Score tiles are transposed (S^T = K Q^T, dP^T = V dO^T).
+template <typename T, int DP, int LOGB>
+__global__ __launch_bounds__(256) void dense_bwd_dq_fast_kernel(DenseArgs a, int n_qtiles) {
+  typedef Mma<T> M;
+  typedef typename M::Frag Frag;
+  constexpr int WAVES = 4;
+  constexpr int NT = kKT;
+  constexpr int NST = NT / 32;
+  constexpr int NDT = DP / 32;
+  constexpr int NKC = DP / M::KW;
+  constexpr int TILE = NT * DP;
+  constexpr int b = 1 << LOGB;
+  __shared__ __attribute__((aligned(16))) T k0s[TILE];
+  __shared__ __attribute__((aligned(16))) T k1s[TILE];
+  __shared__ __attribute__((aligned(16))) T v0s[TILE];
+  __shared__ __attribute__((aligned(16))) T v1s[TILE];
+  __shared__ int range[2];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 31, half = lane >> 5;
+  const int BH = a.B * a.H;
+  const int bh = blockIdx.x % BH;
+  const int qt = n_qtiles - 1 - (int)(blockIdx.x / BH);  // longest causal rows first
+  const int bi = bh / a.H, hh = bh % a.H;
+  const int row = qt * 32 * WAVES + wave * 32 + col;
+  const bool row_in = row < a.Q;
+  const int64_t H = a.H, D = a.D, N = a.N;
+  const int64_t p = row_in ? a.pos[(int64_t)bi * a.Q + row] : -1;
+
+  // remote keys [0, rlim), local keys [rlim, lhi]; bases of the exponents
+  // (+inf for rows without any key, so that every u of theirs is 0)
+  int rlim = 0, lhi = -1;
+  float base_r = kInf, base_l = kInf, ezrz = 0.f, dl = 0.f, rho = 0.f;
+  if (p >= 0) {
+    const int64_t c = p >> LOGB;
+    const int64_t lo = (c - 1) * b > 0 ? (c - 1) * b : 0;
+    rlim = (int)(lo < N ? lo : N);
+    lhi = (int)(p < N - 1 ? p : N - 1);
+    const int64_t sidx = ((int64_t)bi * a.Q + row) * H + hh;
+    const float zr = a.zr[sidx], z = a.z[sidx];
+    base_l = z * kLog2e;
+    if (zr != kNegInf) {
+      base_r = zr * kLog2e;
+      ezrz = __expf(zr - z);
+    }
+    dl = a.delta[sidx];
+    rho = a.rho[sidx];
+  }
+  if (threadIdx.x == 0) { range[0] = -1; range[1] = 0x7fffffff; }
+  __syncthreads();
+  if (lhi >= 0) { atomicMax(&range[0], lhi); atomicMin(&range[1], rlim); }
+  __syncthreads();
+  const int n_tiles = range[0] >= 0 ? range[0] / NT + 1 : 0;
+  // tiles below every valid row's remote limit: all keys remote, no masks
+  const int full = range[1] == 0x7fffffff ? 0 : range[1] / NT;
+
+  const T* kg = reinterpret_cast<const T*>(a.k) + ((int64_t)bi * N * H + hh) * D;
+  const T* vg = reinterpret_cast<const T*>(a.v) + ((int64_t)bi * N * H + hh) * D;
+  const int64_t kstride = H * D;
+  const Stager<T, DP, WAVES> stager(kstride);
+  auto stage = [&]<int BUF>(int i) {
+    stager.template stage<NT>(BUF ? k1s : k0s, kg, kstride, i * NT, a.N);
+    stager.template stage<NT>(BUF ? v1s : v0s, vg, kstride, i * NT, a.N);
+  };
+  if (n_tiles > 0) stage.template operator()<0>(0);
+
+  const int64_t obase = (((int64_t)bi * a.Q + (row_in ? row : 0)) * H + hh) * D;
+  Frag qf[NKC], gf[NKC];
+  {
+    const T* qrow = reinterpret_cast<const T*>(a.q) + obase;
+    const T* grow = reinterpret_cast<const T*>(a.dout) + obase;
+#pragma unroll
+    for (int c = 0; c < NKC; ++c) {
+      qf[c] = row_in ? *reinterpret_cast<const Frag*>(qrow + c * 16 + half * 8) : Frag{};
+      gf[c] = row_in ? *reinterpret_cast<const Frag*>(grow + c * 16 + half * 8) : Frag{};
+    }
+  }
+
+  // per-lane LDS fragment offsets (see dense_fwd_fast.hip)
+  int koff[NKC];
+#pragma unroll
+  for (int c = 0; c < NKC; ++c) koff[c] = col * DP + (((2 * c + half) ^ swz<DP>(col)) * 8);
+  int toff[NDT];
+  {
+    const int gi = lane >> 4, sl = lane & 15;
+    const int r0 = 4 * (gi >> 1) + (sl >> 2);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const int d = 32 * dt + 16 * (gi & 1) + 4 * (sl & 3);
+      toff[dt] = r0 * DP + (((d >> 3) ^ swz<DP>(r0)) * 8) + (d & 7);
+    }
+  }
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  typedef short s8 __attribute__((ext_vector_type(8)));
+  auto rfrag = [&](const T* buf, int st, int c) -> Frag {
+    return *reinterpret_cast<const Frag*>(buf + 32 * st * DP + koff[c]);
+  };
+  auto tfrag = [&](const T* buf, int k0, int dt) -> Frag {
+    const T* p0 = buf + k0 * DP + toff[dt];
+    s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)p0);
+    s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(p0 + 8 * DP));
+    return __builtin_bit_cast(Frag, (s8)__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+
+  f32x16 acc[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) acc[dt] = zero16();
+  float2* tab = a.tab + (int64_t)bh * a.nblk * a.Qp;
+  const float c2 = a.scale_log2;
+
+  auto step = [&]<int BUF, bool FULL>(int i) {
+    const int kb = i * NT;
+    wait_vm();
+    __syncthreads();
+    if (i + 1 < n_tiles) stage.template operator()<1 - BUF>(i + 1);
+    const T* kt = BUF ? k1s : k0s;
+    const T* vt = BUF ? v1s : v0s;
+
+    f32x16 s[NST], dp[NST];
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+      f32x16 x = zero16(), y = zero16();
+#pragma unroll
+      for (int c = 0; c < NKC; ++c) {
+        x = M::mma(rfrag(kt, st, c), qf[c], x);
+        y = M::mma(rfrag(vt, st, c), gf[c], y);
+      }
+      s[st] = x;
+      dp[st] = y;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // key of register r in subtile st: kb + 4*half + off(st, r)
+    const int base_k = kb + 4 * half;
+    const int lim_r = rlim - base_k;     // remote iff off < lim_r
+    const int lim_v = lhi + 1 - base_k;  // visible iff off < lim_v
+    auto offset = [](int st, int r) { return 32 * st + 8 * (r >> 2) + (r & 3); };
+    // u
+#pragma unroll
+    for (int st = 0; st < NST; ++st)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        if constexpr (FULL) {
+          s[st][r] = fast_exp2(fmaf(s[st][r], c2, -base_r));
+        } else {
+          const int off = offset(st, r);
+          const float x = fmaf(s[st][r], c2, off < lim_r ? -base_r : -base_l);
+          s[st][r] = off < lim_v ? fast_exp2(x) : 0.f;
+        }
+      }
+    // U_j, then direct = P (dP - delta) with P = u U_j e^{ZR-Z} (remote) or u
+    float ub[NST][8];
+    block_sums<NST, LOGB>(s, ub);
+#pragma unroll
+    for (int st = 0; st < NST; ++st)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float ur = ub[st][blk_slot<LOGB>(r)] * ezrz;
+        float mult;
+        if constexpr (FULL) mult = ur;
+        else mult = offset(st, r) < lim_r ? ur : 1.f;
+        dp[st][r] = s[st][r] * mult * (dp[st][r] - dl);
+      }
+    float gb[NST][8];
+    block_sums<NST, LOGB>(dp, gb);
+    // gate coefficient per block: G_j / U_j - rho (0 where U_j = 0: every u is 0)
+    constexpr int NS = BlkSlots<LOGB>::n;
+#pragma unroll
+    for (int st = 0; st < NST; ++st)
+#pragma unroll
+      for (int j = 0; j < NS; ++j) gb[st][j] = ub[st][j] > 0.f ? gb[st][j] / ub[st][j] - rho : 0.f;
+#pragma unroll
+    for (int st = 0; st < NST; ++st)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float g = gb[st][blk_slot<LOGB>(r)];
+        if constexpr (FULL) dp[st][r] = fmaf(s[st][r], g, dp[st][r]);
+        else dp[st][r] = offset(st, r) < lim_r ? fmaf(s[st][r], g, dp[st][r]) : dp[st][r];
+      }
+    // table entries of this tile's blocks (one writer per row and block)
+    if (row_in && (BlkSlots<LOGB>::per_half || half == 0)) {
+      constexpr int STEP = LOGB >= 5 ? ((1 << LOGB) / 32 < NST ? (1 << LOGB) / 32 : NST) : 1;
+#pragma unroll
+      for (int st = 0; st < NST; st += STEP)
+#pragma unroll
+        for (int j = 0; j < NS; ++j) {
+          const int bl = (kb >> LOGB) + blk_index<LOGB>(st, j, half);
+          const int ks = bl << LOGB;
+          float beta, eps;
+          if (FULL || ks < rlim) {
+            const float u = ub[st][j];
+            beta = base_l - fast_log2(u);
+            const float w = u * ezrz;
+            float gam = w > 0.f ? gb[st][j] / w : 0.f;
+            gam = fabsf(gam) <= 3.0e38f ? gam : 0.f;  // overflow only where P_i is 0
+            eps = gam - dl;
+          } else if (ks <= lhi) {
+            beta = base_l;
+            eps = -dl;
+          } else {
+            beta = kInf;
+            eps = 0.f;
+          }
+          tab[(int64_t)bl * a.Qp + row] = make_float2(beta, eps);
+        }
+    }
+    // dQ^T += K^T dA^T
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const Frag bd = frag_from_c<T>(dp[st], h2);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) acc[dt] = M::mma(tfrag(kt, 32 * st + 16 * h2, dt), bd, acc[dt]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto run = [&]<int BUF>(int i) {
+    if (i < full) step.template operator()<BUF, true>(i);
+    else step.template operator()<BUF, false>(i);
+  };
+  for (int i = 0; i < n_tiles; i += 2) {
+    run.template operator()<0>(i);
+    if (i + 1 < n_tiles) run.template operator()<1>(i + 1);
+  }
+  if (!row_in) return;
+  T* dq = reinterpret_cast<T*>(a.dq) + obase;
+  typedef T T4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      T4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = from_float<T>(acc[dt][4 * i + j] * a.scale);
+      *reinterpret_cast<T4*>(dq + 32 * dt + 8 * i + 4 * half) = o;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// dK and dV. A workgroup owns 128 keys of one (batch, head) (wave w: keys
+// 32w..32w+31, lane = key) and walks the 64-row query tiles that see any of
+// them. Score tiles are S = Q K^T and dP = dO V^T (lane = key), K and V
+// fragments stay in registers; dV^T += dO^T P and dK^T += Q^T dA take the
+// transposed operands from the staged tiles.
+template <typename T, int DP, int LOGB>
+__global__ __launch_bounds__(256) void dense_bwd_dkv_fast_kernel(DenseArgs a, int n_rtiles) {
+  typedef Mma<T> M;
+  typedef typename M::Frag Frag;
+  constexpr int WAVES = 4;
+  constexpr int MQ = kRT;
+  constexpr int NRS = MQ / 32;
+  constexpr int NDT = DP / 32;
+  constexpr int NKC = DP / M::KW;
+  constexpr int QTILE = MQ * DP;
+  constexpr int NB = (kKT >> LOGB) > 0 ? (kKT >> LOGB) : 1;  // key blocks per workgroup
+  __shared__ __attribute__((aligned(16))) T q0s[QTILE];
+  __shared__ __attribute__((aligned(16))) T q1s[QTILE];
+  __shared__ __attribute__((aligned(16))) T g0s[QTILE];
+  __shared__ __attribute__((aligned(16))) T g1s[QTILE];
+  __shared__ __attribute__((aligned(16))) float2 t0s[NB * MQ];
+  __shared__ __attribute__((aligned(16))) float2 t1s[NB * MQ];
+  __shared__ __attribute__((aligned(16))) int l0s[MQ];
+  __shared__ __attribute__((aligned(16))) int l1s[MQ];
+  __shared__ int list[kMaxRTiles];
+  __shared__ int count;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 31, half = lane >> 5;
+  const int BH = a.B * a.H;
+  const int bh = blockIdx.x % BH;
+  const int kt_idx = (int)(blockIdx.x / BH);  // ascending: the first key tiles see the most rows
+  const int bi = bh / a.H, hh = bh % a.H;
+  const int kb = kt_idx * kKT;
+  const int key = kb + 32 * wave + col;
+  const int64_t H = a.H, D = a.D, N = a.N;
+  const int64_t kstride = H * D;
+
+  // row tiles that see a key of this workgroup, in order; bit 0 marks tiles
+  // whose rows all see every key of it (no masks)
+  if (wave == 0) {
+    const int* tmax = a.tmax + (int64_t)bi * n_rtiles;
+    const int* tmin = a.tmin + (int64_t)bi * n_rtiles;
+    int n = 0;
+    for (int c0 = 0; c0 < n_rtiles; c0 += 64) {
+      const int t = c0 + lane;
+      const int mx = t < n_rtiles ? tmax[t] : -1;
+      const int mn = t < n_rtiles ? tmin[t] : -1;
+      const bool act = mx >= kb;
+      const uint64_t m = __ballot(act);
+      const int before = __popcll(m & ((uint64_t(1) << lane) - 1));
+      if (act) list[n + before] = 2 * t + (mn >= kb + kKT - 1 ? 1 : 0);
+      n += __popcll(m);
+    }
+    if (lane == 0) count = n;
+  }
+
+  const T* kg = reinterpret_cast<const T*>(a.k) + ((int64_t)bi * N * H + hh) * D;
+  const T* vg = reinterpret_cast<const T*>(a.v) + ((int64_t)bi * N * H + hh) * D;
+  Frag kf[NKC], vf[NKC];
+  {
+    const bool key_in = key < a.N;
+    const T* krow = kg + (int64_t)(key_in ? key : 0) * kstride;
+    const T* vrow = vg + (int64_t)(key_in ? key : 0) * kstride;
+#pragma unroll
+    for (int c = 0; c < NKC; ++c) {
+      kf[c] = key_in ? *reinterpret_cast<const Frag*>(krow + c * 16 + half * 8) : Frag{};
+      vf[c] = key_in ? *reinterpret_cast<const Frag*>(vrow + c * 16 + half * 8) : Frag{};
+    }
+  }
+  __syncthreads();
+  const int n_act = count;
+
+  const T* qg = reinterpret_cast<const T*>(a.q) + ((int64_t)bi * a.Q * H + hh) * D;
+  const T* gg = reinterpret_cast<const T*>(a.dout) + ((int64_t)bi * a.Q * H + hh) * D;
+  const float2* tg = a.tab + ((int64_t)bh * a.nblk + (int64_t)kt_idx * NB) * a.Qp;
+  const int* lg = a.lim + (int64_t)bi * a.Qp;
+  const Stager<T, DP, WAVES> stager(kstride);
+  auto stage = [&]<int BUF>(int idx) {
+    const int m0 = (list[idx] >> 1) * MQ;
+    stager.template stage<MQ>(BUF ? q1s : q0s, qg, kstride, m0, a.Q);
+    stager.template stage<MQ>(BUF ? g1s : g0s, gg, kstride, m0, a.Q);
+    // table slice: NB blocks x 64 rows of (beta, eps), 512 contiguous bytes
+    // per block; 16 bytes (two rows) per lane
+    char* tl = reinterpret_cast<char*>(BUF ? t1s : t0s);
+#pragma unroll
+    for (int j0 = 0; j0 < NB * 32; j0 += 256) {
+      const int j = j0 + (int)threadIdx.x;
+      if (j < NB * 32)
+        async_copy16(tg + (int64_t)(j >> 5) * a.Qp + m0 + 2 * (j & 31), tl + (j0 + 64 * wave) * 16);
+    }
+    if (threadIdx.x < 16) async_copy16(lg + m0 + 4 * threadIdx.x, BUF ? l1s : l0s);
+  };
+  if (n_act > 0) stage.template operator()<0>(0);
+
+  int qoff[NKC];
+#pragma unroll
+  for (int c = 0; c < NKC; ++c) qoff[c] = col * DP + (((2 * c + half) ^ swz<DP>(col)) * 8);
+  int toff[NDT];
+  {
+    const int gi = lane >> 4, sl = lane & 15;
+    const int r0 = 4 * (gi >> 1) + (sl >> 2);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const int d = 32 * dt + 16 * (gi & 1) + 4 * (sl & 3);
+      toff[dt] = r0 * DP + (((d >> 3) ^ swz<DP>(r0)) * 8) + (d & 7);
+    }
+  }
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  typedef short s8 __attribute__((ext_vector_type(8)));
+  auto rfrag = [&](const T* buf, int rs, int c) -> Frag {
+    return *reinterpret_cast<const Frag*>(buf + 32 * rs * DP + qoff[c]);
+  };
+  auto tfrag = [&](const T* buf, int k0, int dt) -> Frag {
+    const T* p0 = buf + k0 * DP + toff[dt];
+    s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)p0);
+    s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(p0 + 8 * DP));
+    return __builtin_bit_cast(Frag, (s8)__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+
+  f32x16 dk[NDT], dv[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) { dk[dt] = zero16(); dv[dt] = zero16(); }
+  const int tcol = ((32 * wave + col) >> LOGB) * MQ;  // this lane's block in the table slice
+  const float c2 = a.scale_log2;
+
+  auto step = [&]<int BUF, bool FULL>(int idx) {
+    wait_vm();
+    __syncthreads();
+    if (idx + 1 < n_act) stage.template operator()<1 - BUF>(idx + 1);
+    const T* qt = BUF ? q1s : q0s;
+    const T* gt = BUF ? g1s : g0s;
+    const float* tt = reinterpret_cast<const float*>((BUF ? t1s : t0s) + tcol);
+    const int* lt = BUF ? l1s : l0s;
+
+    f32x16 s[NRS], dp[NRS];
+#pragma unroll
+    for (int rs = 0; rs < NRS; ++rs) {
+      f32x16 x = zero16(), y = zero16();
+#pragma unroll
+      for (int c = 0; c < NKC; ++c) {
+        x = M::mma(rfrag(qt, rs, c), kf[c], x);
+        y = M::mma(rfrag(gt, rs, c), vf[c], y);
+      }
+      s[rs] = x;
+      dp[rs] = y;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // register r of row subtile rs holds row 32rs + 8(r/4) + 4half + r%4
+#pragma unroll
+    for (int rs = 0; rs < NRS; ++rs)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r0 = 32 * rs + 8 * i + 4 * half;
+        const f32x4 t01 = *reinterpret_cast<const f32x4*>(tt + 2 * r0);
+        const f32x4 t23 = *reinterpret_cast<const f32x4*>(tt + 2 * r0 + 4);
+        const float beta[4] = {t01[0], t01[2], t23[0], t23[2]};
+        const float eps[4] = {t01[1], t01[3], t23[1], t23[3]};
+        int lim[4] = {0, 0, 0, 0};
+        if constexpr (!FULL) {
+          typedef int i4 __attribute__((ext_vector_type(4)));
+          const i4 l4 = *reinterpret_cast<const i4*>(lt + r0);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) lim[j] = l4[j];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = 4 * i + j;
+          const float pv = fast_exp2(fmaf(s[rs][r], c2, -beta[j]));
+          const float da = pv * (dp[rs][r] + eps[j]);
+          if constexpr (FULL) {
+            s[rs][r] = pv;
+            dp[rs][r] = da;
+          } else {
+            const bool vis = key <= lim[j];
+            s[rs][r] = vis ? pv : 0.f;
+            dp[rs][r] = vis ? da : 0.f;
+          }
+        }
+      }
+    // dV^T += dO^T P, dK^T += Q^T dA (row order permuted as in frag_from_c)
+#pragma unroll
+    for (int rs = 0; rs < NRS; ++rs)
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const Frag bp = frag_from_c<T>(s[rs], h2);
+        const Frag bd = frag_from_c<T>(dp[rs], h2);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          dv[dt] = M::mma(tfrag(gt, 32 * rs + 16 * h2, dt), bp, dv[dt]);
+          dk[dt] = M::mma(tfrag(qt, 32 * rs + 16 * h2, dt), bd, dk[dt]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+  };
+  auto run = [&]<int BUF>(int idx) {
+    if (list[idx] & 1) step.template operator()<BUF, true>(idx);
+    else step.template operator()<BUF, false>(idx);
+  };
+  for (int idx = 0; idx < n_act; idx += 2) {
+    run.template operator()<0>(idx);
+    if (idx + 1 < n_act) run.template operator()<1>(idx + 1);
+  }
+  if (key >= a.N) return;
+  const int64_t kbase = (((int64_t)bi * N + key) * H + hh) * D;
+  T* dkp = reinterpret_cast<T*>(a.dk) + kbase;
+  T* dvp = reinterpret_cast<T*>(a.dv) + kbase;
+  typedef T T4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      T4 ok, ov;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        ok[j] = from_float<T>(dk[dt][4 * i + j] * a.scale);
+        ov[j] = from_float<T>(dv[dt][4 * i + j]);
+      }
+      *reinterpret_cast<T4*>(dkp + 32 * dt + 8 * i + 4 * half) = ok;
+      *reinterpret_cast<T4*>(dvp + 32 * dt + 8 * i + 4 * half) = ov;
+    }
+}
+
+template <typename T, int DP>
+static hipError_t launch_fast(const DenseArgs& a, hipStream_t stream) {
+  const int n_rows = a.B * a.Qp;
+  hipLaunchKernelGGL(dense_bwd_rows_kernel, dim3((n_rows + 255) / 256), dim3(256), 0, stream, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int n_qtiles = (a.Q + 127) / 128;
+  const int n_ktiles = (a.N + kKT - 1) / kKT;
+  const int n_rtiles = a.Qp / kRT;
+  const unsigned BH = (unsigned)(a.B * a.H);
+  auto go = [&]<int LOGB>() {
+    hipLaunchKernelGGL((dense_bwd_dq_fast_kernel<T, DP, LOGB>), dim3(n_qtiles * BH), dim3(256), 0, stream, a,
+                       n_qtiles);
+    if (hipPeekAtLastError() != hipSuccess) return;
+    hipLaunchKernelGGL((dense_bwd_dkv_fast_kernel<T, DP, LOGB>), dim3(n_ktiles * BH), dim3(256), 0, stream, a,
+                       n_rtiles);
+  };
+  switch (a.logb) {
+    case 1: go.template operator()<1>(); break;
+    case 2: go.template operator()<2>(); break;
+    case 3: go.template operator()<3>(); break;
+    case 4: go.template operator()<4>(); break;
+    case 5: go.template operator()<5>(); break;
+    case 6: go.template operator()<6>(); break;
+    default: go.template operator()<7>(); break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_dense_bwd_fast(int dtype, const DenseArgs& a, hipStream_t stream) {
+  if (dtype == kBF16) return a.D == 64 ? launch_fast<bf16, 64>(a, stream) : launch_fast<bf16, 128>(a, stream);
+  return a.D == 64 ? launch_fast<f16, 64>(a, stream) : launch_fast<f16, 128>(a, stream);
+}
+
+}  // namespace st

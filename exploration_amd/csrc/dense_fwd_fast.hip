@@ -71,10 +71,11 @@ __global__ __launch_bounds__(256) void dense_fwd_fast_kernel(DenseArgs a, int n_
   const T* kg = reinterpret_cast<const T*>(a.k) + ((int64_t)bi * N * H + hh) * D;
   const T* vg = reinterpret_cast<const T*>(a.v) + ((int64_t)bi * N * H + hh) * D;
   const int64_t kstride = H * D;
+  const Stager<T, DP, WAVES> stager(kstride);
   auto stage = [&]<int BUF>(int i) {
     const int kb = tile_of(i) * NT;
-    stage_async<T, NT, DP, WAVES>(BUF ? k1s : k0s, kg, kstride, kb, a.N, a.D);
-    stage_async<T, NT, DP, WAVES>(BUF ? v1s : v0s, vg, kstride, kb, a.N, a.D);
+    stager.template stage<NT>(BUF ? k1s : k0s, kg, kstride, kb, a.N);
+    stager.template stage<NT>(BUF ? v1s : v0s, vg, kstride, kb, a.N);
   };
   if (total > 0) stage.template operator()<0>(0);
 

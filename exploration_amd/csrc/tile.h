@@ -232,30 +232,52 @@ template <int LOGB> struct BlkSlots {
 //    fragments) hit 4 distinct 32-byte bank groups.
 template <int DP> __device__ __forceinline__ int swz(int r) { return 2 * (r % (DP / 16)); }
 
-// Issue the asynchronous copies of rows [r0, r0+ROWS) x [0, DP) of a
-// [*, stride] matrix into a swizzled LDS tile; rows >= nrows re-read row
-// nrows-1 and chunks at or beyond ncols re-read chunk 0 (finite data whose
-// products are masked or discarded). Every wave of the workgroup takes part.
-template <typename T, int ROWS, int DP, int NWAVES>
-__device__ __forceinline__ void stage_async(T* lds, const T* g, int64_t stride, int r0, int nrows,
-                                            int ncols) {
+// Asynchronous copies of full-width row tiles (rows [r0, r0+ROWS) x [0, DP)
+// of a [*, stride] matrix with DP columns) into the swizzled LDS layout. One
+// instruction of the NWAVES waves moves a slab of RPI rows, and a lane's
+// position within a slab (row, swizzled chunk) is the same for every slab, so
+// its byte offset is computed once: a slab inside the matrix is a wave-uniform
+// base address plus that 32-bit offset. In a slab that crosses row nrows the
+// rows at or beyond it re-read row nrows-1 (finite data whose products are
+// masked or discarded). Every wave of the workgroup takes part.
+template <typename T, int DP, int NWAVES> struct Stager {
   static_assert(sizeof(T) == 2, "16-bit tiles");
-  constexpr int CPR = DP / 8;
-  constexpr int SLOTS = ROWS * CPR;
-  static_assert(SLOTS % (64 * NWAVES) == 0, "tile must split evenly over the waves");
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int it = 0; it < SLOTS / (64 * NWAVES); ++it) {
-    const int base = (it * NWAVES + wave) * 64;
-    const int p = base + lane;
-    const int r = p / CPR;
-    int c = (p % CPR) ^ swz<DP>(r);
-    if (c * 8 >= ncols) c = 0;
-    int row = r0 + r;
-    row = row < nrows ? row : nrows - 1;
-    async_copy16(g + (int64_t)row * stride + c * 8, lds + base * 8);
+  static constexpr int CPR = DP / 8;                // 16-byte chunks per row
+  static constexpr int RPI = NWAVES * 64 / CPR;     // rows per slab
+  static_assert(RPI % (DP / 16) == 0, "a slab must keep the swizzle phase");
+  int r_lane, chunk;
+  uint32_t off;
+  __device__ __forceinline__ explicit Stager(int64_t stride) {
+    const int p = (int)threadIdx.x;
+    r_lane = p / CPR;
+    chunk = (p % CPR) ^ swz<DP>(r_lane);
+    off = (uint32_t)(((int64_t)r_lane * stride + chunk * 8) * (int64_t)sizeof(T));
   }
-}
+  template <int ROWS>
+  __device__ __forceinline__ void stage(T* lds, const T* g, int64_t stride, int r0, int nrows) const {
+    static_assert(ROWS % RPI == 0, "tile must split into whole slabs");
+    // wave-uniform (scalar) so that the LDS destinations are scalar too
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (r0 + ROWS <= nrows) {
+#pragma unroll
+      for (int it = 0; it < ROWS / RPI; ++it) {
+        const char* base = reinterpret_cast<const char*>(g + (int64_t)(r0 + it * RPI) * stride);
+        async_copy16(base + off, lds + (it * NWAVES + wave) * 64 * 8);
+      }
+    } else {
+      // recomputed per call: hoisting r_lane + it*RPI out of the caller's
+      // loop would hold (or spill) one register per slab
+      int rl = r_lane;
+      __asm__ volatile("" : "+v"(rl));
+#pragma unroll
+      for (int it = 0; it < ROWS / RPI; ++it) {
+        int row = r0 + it * RPI + rl;
+        row = row < nrows ? row : nrows - 1;
+        async_copy16(g + (int64_t)row * stride + chunk * 8, lds + (it * NWAVES + wave) * 64 * 8);
+      }
+    }
+  }
+};
 
 // MFMA fragment (8 elements) of swizzled row n, logical chunk c.
 template <typename T, int DP>
@@ -287,12 +309,8 @@ __device__ __forceinline__ typename Mma<T>::Frag frag_tr(const T* lds, int k0, i
   return __builtin_bit_cast(typename Mma<T>::Frag, v);
 }
 
-// Half-wave exchange on gfx950 without the LDS crossbar: returns x of the
-// lane 32 positions away.
-__device__ __forceinline__ float swap_halves(float x) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
-}
+// Half-wave exchange: returns x of the lane 32 positions away.
+__device__ __forceinline__ float swap_halves(float x) { return other_half(x); }
 
 // Runs body.template operator()<LOGB>() for the runtime block size.
 template <typename F> __device__ __forceinline__ void dispatch_logb(int logb, F&& body) {

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ST_ABI_VERSION 1
+#define ST_ABI_VERSION 2
 
 #define ST_DTYPE_F32 0
 #define ST_DTYPE_F16 1
@@ -64,8 +64,15 @@ int st_dense_fwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_
                  const void* v, const int64_t* positions, void* out, float* rc, float* pr,
                  float* zr, float* z, void* stream);
 
-/* Bytes of device workspace st_dense_bwd needs (delta and rho). */
-size_t st_dense_bwd_workspace_bytes(int64_t batch, int64_t queries, int64_t heads);
+/* Bytes of device workspace st_dense_bwd needs for this problem (0 if the
+ * arguments are invalid): per-row delta and rho, plus, on the pipelined
+ * 16-bit path (head_dim 64 or 128), row limits and a per-(row, key block)
+ * table of 8 bytes, B*H*ceil(Q/64)*64*ceil(N/128)*(128/block_size) entries,
+ * capped at 4 GiB (larger problems take the generic kernels). No reference
+ * counterpart: the reference's Triton backward allocates its own buffers
+ * (st/ops/kernels/dense.py:221-233). */
+size_t st_dense_bwd_workspace_bytes(int dtype, int64_t batch, int64_t queries, int64_t keys,
+                                    int64_t heads, int64_t head_dim, int64_t block_size);
 
 /* Gated dense backward (first derivatives). Replaces the `_preprocess`,
  * `_backward_q` and `_backward_kv` launches of st/ops/kernels/dense.py:221-233.

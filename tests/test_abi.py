@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in declared_functions():
         assert hasattr(lib, name), f"{name} missing from libst_attn.so"
-    assert lib.st_abi_version() == 1
+    assert lib.st_abi_version() == 2
     assert lib.st_last_error() == b""
 
 
@@ -67,7 +67,12 @@ def test_argument_errors_map_to_value_error():
     status = lib.st_sparse_fwd(2, 1, 1, 1, 64, 16, 4, null, null, ctypes.c_void_p(16), null, null, 16, 1,
                                100, 8, null, null, null, null, null, null, 0, null)
     assert status == _lib.ST_EINVAL and b"block aligned" in lib.st_last_error()
-    assert lib.st_dense_bwd_workspace_bytes(2, 5, 3) == 2 * 256
+    # fp32: delta and rho only; bf16 head_dim 64: plus row limits, row-tile
+    # statistics and the (beta, eps) table (B*H*Qp*nblk*8 bytes)
+    assert lib.st_dense_bwd_workspace_bytes(0, 2, 5, 7, 3, 64, 4) == 2 * 256
+    # delta+rho 2*256, lim [2, 64] int32 512, tmin/tmax 2*256, table 2*3 heads x 32 blocks x 64 rows
+    assert lib.st_dense_bwd_workspace_bytes(2, 2, 5, 7, 3, 64, 4) == 2 * 256 + 512 + 2 * 256 + 2 * 3 * 32 * 64 * 8
+    assert lib.st_dense_bwd_workspace_bytes(2, 2, 5, 7, 3, 64, 3) == 0
 
 
 def test_python_entry_points_validate_like_the_reference():

@@ -92,6 +92,29 @@ def test_unsorted_positions_and_padding(device, dtype):
     _check_dense(q, k, v, pos, probe, b, device, dtype, label="unsorted")
 
 
+FAST_CASES = [(64, 2), (64, 4), (64, 8), (64, 16), (64, 64), (64, 128), (128, 16), (128, 32), (128, 64),
+              (128, 128)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("d,b", FAST_CASES)
+def test_pipelined_path_block_sizes(device, d, b, dtype):
+    """16-bit head_dim 64/128 (the pipelined kernels) at every block size:
+    batch 2, 3 heads, 300 keys (a partial last key tile), 140 query rows
+    (three 64-row tiles, the last partial) with unsorted positions, padding
+    rows, a row at key 0 and rows past the last key."""
+    print(f"dense pipelined d={d} b={b} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(11 + d + b)
+    n, rows = 300, 140
+    q = torch.randn(2, rows, 3, d, generator=g).to(dtype)
+    k = torch.randn(2, n, 3, d, generator=g).to(dtype)
+    v = torch.randn(2, n, 3, d, generator=g).to(dtype)
+    probe = torch.randn(2, rows, 3, d, generator=g).to(dtype)
+    pos = torch.randint(-1, n + 40, (2, rows), generator=g)
+    pos[0, :4] = torch.tensor([0, -1, n - 1, n + 5])
+    _check_dense(q, k, v, pos, probe, b, device, dtype, label=f"pipelined d={d} b={b}")
+
+
 def test_cfg5_shaped_chunk(device):
     """cfg5 G-round shape: bf16, H16 D64 b16, 240 supervised query positions
     over N=8192 keys (oracle in float32 on the GPU)."""
