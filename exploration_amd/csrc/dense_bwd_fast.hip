@@ -101,7 +101,7 @@ __global__ __launch_bounds__(256) void dense_bwd_rows_kernel(DenseArgs a) {
 // 32w..32w+31, lane = row) of one (batch, head) and walks the key tiles of
 // its causal range. Score tiles are transposed (S^T = K Q^T, dP^T = V dO^T).
 template <typename T, int DP, int LOGB>
-__global__ __launch_bounds__(256) void dense_bwd_dq_fast_kernel(DenseArgs a, int n_qtiles) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void dense_bwd_dq_fast_kernel(DenseArgs a, int n_qtiles) {
   typedef Mma<T> M;
   typedef typename M::Frag Frag;
   constexpr int WAVES = 4;
@@ -219,17 +219,15 @@ __global__ __launch_bounds__(256) void dense_bwd_dq_fast_kernel(DenseArgs a, int
 
     f32x16 s[NST], dp[NST];
 #pragma unroll
-    for (int st = 0; st < NST; ++st) {
-      f32x16 x = zero16(), y = zero16();
-#pragma unroll
-      for (int c = 0; c < NKC; ++c) {
-        x = M::mma(rfrag(kt, st, c), qf[c], x);
-        y = M::mma(rfrag(vt, st, c), gf[c], y);
-      }
-      s[st] = x;
-      dp[st] = y;
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    for (int st = 0; st < NST; ++st) { s[st] = zero16(); dp[st] = zero16(); }
+    // product j: subtile j / (2 NKC), chunk (j / 2) % NKC, S (even j) or dP (odd j)
+    mfma_phase<NST * 2 * NKC, 4, 1>(
+        [&](int j) { return rfrag((j & 1) ? vt : kt, j / (2 * NKC), (j >> 1) % NKC); },
+        [&](int j, Frag f) {
+          const int st = j / (2 * NKC), c = (j >> 1) % NKC;
+          if (j & 1) dp[st] = M::mma(f, gf[c], dp[st]);
+          else s[st] = M::mma(f, qf[c], s[st]);
+        });
     // key of register r in subtile st: kb + 4*half + off(st, r)
     const int base_k = kb + 4 * half;
     const int lim_r = rlim - base_k;     // remote iff off < lim_r
@@ -305,16 +303,15 @@ __global__ __launch_bounds__(256) void dense_bwd_dq_fast_kernel(DenseArgs a, int
         }
     }
     // dQ^T += K^T dA^T
+    Frag bd[NST][2];
 #pragma unroll
-    for (int st = 0; st < NST; ++st) {
+    for (int st = 0; st < NST; ++st)
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const Frag bd = frag_from_c<T>(dp[st], h2);
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) acc[dt] = M::mma(tfrag(kt, 32 * st + 16 * h2, dt), bd, acc[dt]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
+      for (int h2 = 0; h2 < 2; ++h2) bd[st][h2] = frag_from_c<T>(dp[st], h2);
+    // product j: 16-key chunk j / NDT, head-dim tile j % NDT
+    mfma_phase<NST * 2 * NDT, 4, 2>(
+        [&](int j) { return tfrag(kt, 16 * (j / NDT), j % NDT); },
+        [&](int j, Frag f) { acc[j % NDT] = M::mma(f, bd[j / (2 * NDT)][(j / NDT) & 1], acc[j % NDT]); });
   };
   auto run = [&]<int BUF>(int i) {
     if (i < full) step.template operator()<BUF, true>(i);
@@ -345,7 +342,7 @@ __global__ __launch_bounds__(256) void dense_bwd_dq_fast_kernel(DenseArgs a, int
 // fragments stay in registers; dV^T += dO^T P and dK^T += Q^T dA take the
 // transposed operands from the staged tiles.
 template <typename T, int DP, int LOGB>
-__global__ __launch_bounds__(256) void dense_bwd_dkv_fast_kernel(DenseArgs a, int n_rtiles) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void dense_bwd_dkv_fast_kernel(DenseArgs a, int n_rtiles) {
   typedef Mma<T> M;
   typedef typename M::Frag Frag;
   constexpr int WAVES = 4;
@@ -476,17 +473,15 @@ __global__ __launch_bounds__(256) void dense_bwd_dkv_fast_kernel(DenseArgs a, in
 
     f32x16 s[NRS], dp[NRS];
 #pragma unroll
-    for (int rs = 0; rs < NRS; ++rs) {
-      f32x16 x = zero16(), y = zero16();
-#pragma unroll
-      for (int c = 0; c < NKC; ++c) {
-        x = M::mma(rfrag(qt, rs, c), kf[c], x);
-        y = M::mma(rfrag(gt, rs, c), vf[c], y);
-      }
-      s[rs] = x;
-      dp[rs] = y;
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    for (int rs = 0; rs < NRS; ++rs) { s[rs] = zero16(); dp[rs] = zero16(); }
+    // product j: row subtile j / (2 NKC), chunk (j / 2) % NKC, S (even j) or dP (odd j)
+    mfma_phase<NRS * 2 * NKC, 4, 1>(
+        [&](int j) { return rfrag((j & 1) ? gt : qt, j / (2 * NKC), (j >> 1) % NKC); },
+        [&](int j, Frag f) {
+          const int rs = j / (2 * NKC), c = (j >> 1) % NKC;
+          if (j & 1) dp[rs] = M::mma(f, vf[c], dp[rs]);
+          else s[rs] = M::mma(f, kf[c], s[rs]);
+        });
     // register r of row subtile rs holds row 32rs + 8(r/4) + 4half + r%4
 #pragma unroll
     for (int rs = 0; rs < NRS; ++rs)
@@ -520,19 +515,23 @@ __global__ __launch_bounds__(256) void dense_bwd_dkv_fast_kernel(DenseArgs a, in
         }
       }
     // dV^T += dO^T P, dK^T += Q^T dA (row order permuted as in frag_from_c)
+    Frag bp[NRS][2], bd[NRS][2];
 #pragma unroll
     for (int rs = 0; rs < NRS; ++rs)
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2) {
-        const Frag bp = frag_from_c<T>(s[rs], h2);
-        const Frag bd = frag_from_c<T>(dp[rs], h2);
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          dv[dt] = M::mma(tfrag(gt, 32 * rs + 16 * h2, dt), bp, dv[dt]);
-          dk[dt] = M::mma(tfrag(qt, 32 * rs + 16 * h2, dt), bd, dk[dt]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+        bp[rs][h2] = frag_from_c<T>(s[rs], h2);
+        bd[rs][h2] = frag_from_c<T>(dp[rs], h2);
       }
+    // product j: 16-row chunk j / (2 NDT), head-dim tile (j / 2) % NDT,
+    // dV (even j, from dO^T) or dK (odd j, from Q^T)
+    mfma_phase<NRS * 2 * 2 * NDT, 4, 2>(
+        [&](int j) { return tfrag((j & 1) ? qt : gt, 16 * (j / (2 * NDT)), (j >> 1) % NDT); },
+        [&](int j, Frag f) {
+          const int ch = j / (2 * NDT), dt = (j >> 1) % NDT;
+          if (j & 1) dk[dt] = M::mma(f, bd[ch >> 1][ch & 1], dk[dt]);
+          else dv[dt] = M::mma(f, bp[ch >> 1][ch & 1], dv[dt]);
+        });
   };
   auto run = [&]<int BUF>(int idx) {
     if (list[idx] & 1) step.template operator()<BUF, true>(idx);

@@ -16,7 +16,7 @@
 namespace st {
 
 template <typename T, int DP, int LOGB>
-__global__ __launch_bounds__(256) void dense_fwd_fast_kernel(DenseArgs a, int n_qtiles) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void dense_fwd_fast_kernel(DenseArgs a, int n_qtiles) {
   typedef Mma<T> M;
   typedef typename M::Frag Frag;
   constexpr int WAVES = 4;
@@ -155,13 +155,10 @@ __global__ __launch_bounds__(256) void dense_fwd_fast_kernel(DenseArgs a, int n_
 
     f32x16 s[NST];
 #pragma unroll
-    for (int st = 0; st < NST; ++st) {
-      f32x16 x = zero16();
-#pragma unroll
-      for (int c = 0; c < NKC; ++c) x = M::mma(kfrag(kt, st, c), qf[c], x);
-      s[st] = x;
-      __builtin_amdgcn_sched_barrier(0);  // bound the fragments in flight
-    }
+    for (int st = 0; st < NST; ++st) s[st] = zero16();
+    // product j: subtile j / NKC, contraction chunk j % NKC
+    mfma_phase<NST * NKC, 4, 1>([&](int j) { return kfrag(kt, j / NKC, j % NKC); },
+                             [&](int j, Frag f) { s[j / NKC] = M::mma(f, qf[j % NKC], s[j / NKC]); });
     // Raw dot products; the scale is applied inside exp2(s*c - m).
     if constexpr (MASKED) {
       // key of register r in subtile st is kb + 4*half + (32*st + 8*(r/4) + r%4):
@@ -227,17 +224,15 @@ __global__ __launch_bounds__(256) void dense_fwd_fast_kernel(DenseArgs a, int n_
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) acc[dt] *= scale_acc;
     m = mn;
+    Frag bp[NST][2];
 #pragma unroll
-    for (int st = 0; st < NST; ++st) {
+    for (int st = 0; st < NST; ++st)
 #pragma unroll
-      for (int c2 = 0; c2 < 2; ++c2) {
-        const Frag bp = frag_from_c<T>(s[st], c2);
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
-          acc[dt] = M::mma(vfrag(vt, 32 * st + 16 * c2, dt), bp, acc[dt]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
+      for (int c2 = 0; c2 < 2; ++c2) bp[st][c2] = frag_from_c<T>(s[st], c2);
+    // product j: 16-key chunk j / NDT, head-dim tile j % NDT
+    mfma_phase<NST * 2 * NDT, 4, 2>(
+        [&](int j) { return vfrag(vt, 16 * (j / NDT), j % NDT); },
+        [&](int j, Frag f) { acc[j % NDT] = M::mma(f, bp[j / (2 * NDT)][(j / NDT) & 1], acc[j % NDT]); });
   };
   auto run = [&]<int BUF>(int i) {
     if (i < n_remote) {

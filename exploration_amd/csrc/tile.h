@@ -309,6 +309,38 @@ __device__ __forceinline__ typename Mma<T>::Frag frag_tr(const T* lds, int k0, i
   return __builtin_bit_cast(typename Mma<T>::Frag, v);
 }
 
+// An MFMA phase of N products whose A operands are read from LDS, run in
+// chunks of L: wait for the reads in flight, issue the reads of chunk g+1,
+// then the L MFMAs of chunk g. The wait is an explicit lgkmcnt(0) at the
+// chunk boundary (with asynchronous global->LDS copies in flight the
+// compiler only ever waits for all LDS reads, so a read issued right before
+// its MFMA would stall it); here every read has a whole chunk of MFMAs to
+// land. load(j) returns the fragment of product j (R LDS reads); mma(j, f)
+// performs it.
+template <int N, int L, int R, typename Load, typename Mfma>
+__device__ __forceinline__ void mfma_phase(Load&& load, Mfma&& mma) {
+  static_assert(N % L == 0, "phase must split into whole chunks");
+  typedef decltype(load(0)) F;
+  F buf[2][L];
+#pragma unroll
+  for (int i = 0; i < L; ++i) buf[0][i] = load(i);
+#pragma unroll
+  for (int g = 0; g < N / L; ++g) {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt untouched
+    __builtin_amdgcn_sched_barrier(0);
+    if (g + 1 < N / L) {
+#pragma unroll
+      for (int i = 0; i < L; ++i) buf[(g + 1) & 1][i] = load((g + 1) * L + i);
+    }
+#pragma unroll
+    for (int i = 0; i < L; ++i) mma(g * L + i, buf[g & 1][i]);
+    if (g + 1 < N / L) __builtin_amdgcn_sched_group_barrier(0x100, L * R, 0);  // the reads first
+    __builtin_amdgcn_sched_group_barrier(0x008, L, 0);                         // then the MFMAs
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // Half-wave exchange: returns x of the lane 32 positions away.
 __device__ __forceinline__ float swap_halves(float x) { return other_half(x); }
 
