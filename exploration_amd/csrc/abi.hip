@@ -147,6 +147,13 @@ int st_dense_bwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_
     a.tmin = reinterpret_cast<int*>(ws + plan.off_tmin);
     a.tmax = reinterpret_cast<int*>(ws + plan.off_tmax);
     a.tab = reinterpret_cast<float2*>(ws + plan.off_tab);
+    a.q_count = reinterpret_cast<int*>(ws + plan.off_qcnt);
+    a.k_count = reinterpret_cast<int*>(ws + plan.off_kcnt);
+    a.q_part = reinterpret_cast<float*>(ws + plan.off_qpart);
+    a.k_part = reinterpret_cast<float*>(ws + plan.off_kpart);
+    // an item longer than half the longest possible one runs as two pieces
+    a.q_split = (plan.n_ktiles + 1) / 2;
+    a.k_split = (plan.n_rtiles + 1) / 2;
     a.Qp = plan.Qp;
     a.nblk = plan.nblk;
   }

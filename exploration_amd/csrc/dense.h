@@ -29,6 +29,13 @@ struct DenseArgs {
   int* tmin;              // [B,Qp/64] min of lim over 64-row tiles
   int* tmax;              // [B,Qp/64] max of lim over 64-row tiles
   float2* tab;            // [B*H, nblk, Qp] per (key block, row): (beta, eps)
+  // long work items run as two pieces whose fp32 partials a merge kernel
+  // adds afterwards (flags zeroed by the rows kernel)
+  int* q_count;           // [B*H*n_qtiles] 1 if the dQ item was split
+  int* k_count;           // [B*H*n_ktiles] 1 if the dK/dV item was split
+  float* q_part;          // dQ partials, [item][piece][wave][register][lane]
+  float* k_part;          // dK/dV partials, same order
+  int q_split, k_split;   // items with more tiles than this run as two pieces
   int B, Q, N, H, D;
   int block, logb;
   int Qp, nblk;           // Q rounded up to 64; key blocks in whole 128-key tiles
@@ -49,8 +56,8 @@ hipError_t launch_dense_bwd(int dtype, const DenseArgs& a, hipStream_t stream);
 // when it applies (16-bit, head_dim 64/128, table within its size cap).
 struct DenseBwdPlan {
   bool fast;
-  int Qp, nblk, n_rtiles;
-  size_t off_rho, off_lim, off_tmin, off_tmax, off_tab, total;
+  int Qp, nblk, n_rtiles, n_qtiles, n_ktiles;
+  size_t off_rho, off_lim, off_tmin, off_tmax, off_tab, off_qcnt, off_kcnt, off_qpart, off_kpart, total;
 };
 DenseBwdPlan dense_bwd_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t H, int64_t D,
                             int64_t block);

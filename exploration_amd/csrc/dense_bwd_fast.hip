@@ -66,15 +66,25 @@ DenseBwdPlan dense_bwd_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t 
   p.off_tmin = p.off_lim + align256(sizeof(int) * (size_t)(B * Qp));
   p.off_tmax = p.off_tmin + align256(sizeof(int) * (size_t)(B * n_rtiles));
   p.off_tab = p.off_tmax + align256(sizeof(int) * (size_t)(B * n_rtiles));
-  p.total = p.off_tab + align256(tab);
+  p.n_qtiles = (int)((Q + 127) / 128);
+  p.n_ktiles = (int)((N + kKT - 1) / kKT);
+  const size_t q_items = (size_t)(B * H) * p.n_qtiles, k_items = (size_t)(B * H) * p.n_ktiles;
+  p.off_qcnt = p.off_tab + align256(tab);
+  p.off_kcnt = p.off_qcnt + align256(sizeof(int) * q_items);
+  p.off_qpart = p.off_kcnt + align256(sizeof(int) * k_items);
+  // per item and piece: 128 rows (keys) x D floats (x2 for dK and dV)
+  p.off_kpart = p.off_qpart + align256(sizeof(float) * q_items * 2 * 128 * (size_t)D);
+  p.total = p.off_kpart + align256(sizeof(float) * k_items * 2 * 2 * 128 * (size_t)D);
   return p;
 }
 
 // ---------------------------------------------------------------------------
 // Per row: the last visible key (min(p, N-1); -1 for padding rows and rows
 // beyond Q); per 64-row tile (one wave) its min and max.
-__global__ __launch_bounds__(256) void dense_bwd_rows_kernel(DenseArgs a) {
+__global__ __launch_bounds__(256) void dense_bwd_rows_kernel(DenseArgs a, int n_qitems, int n_kitems) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  for (int64_t i = idx; i < n_qitems; i += (int64_t)gridDim.x * 256) a.q_count[i] = 0;
+  for (int64_t i = idx; i < n_kitems; i += (int64_t)gridDim.x * 256) a.k_count[i] = 0;
   // B*Qp is a multiple of 64: whole waves leave together
   if (idx >= (int64_t)a.B * a.Qp) return;
   const int bi = (int)(idx / a.Qp), row = (int)(idx % a.Qp);
@@ -94,6 +104,21 @@ __global__ __launch_bounds__(256) void dense_bwd_rows_kernel(DenseArgs a) {
     a.tmax[idx / kRT] = mx;
     a.tmin[idx / kRT] = mn;
   }
+}
+
+// A piece of a split item stores its fp32 accumulators in register order
+// ([piece][wave][register][lane], so a wave's stores are lane-contiguous);
+// dense_bwd_merge adds the two pieces after the kernel. The first piece
+// marks the item as split.
+template <int NACC>
+__device__ __forceinline__ void store_piece(const f32x16 (&acc)[NACC], float* part, int piece, int* flag) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float* mine = part + ((size_t)piece * 4 + wave) * (NACC * 16 * 64);
+#pragma unroll
+  for (int t = 0; t < NACC; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mine[(t * 16 + r) * 64 + lane] = acc[t][r];
+  if (piece == 0 && threadIdx.x == 0) *flag = 1;
 }
 
 // ---------------------------------------------------------------------------
@@ -121,7 +146,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int col = lane & 31, half = lane >> 5;
   const int BH = a.B * a.H;
   const int bh = blockIdx.x % BH;
-  const int qt = n_qtiles - 1 - (int)(blockIdx.x / BH);  // longest causal rows first
+  // all first pieces (longest causal rows first), then all second pieces
+  const int kq = (int)(blockIdx.x / BH);
+  const int piece = kq >= n_qtiles;
+  const int qt = n_qtiles - 1 - (piece ? kq - n_qtiles : kq);
   const int bi = bh / a.H, hh = bh % a.H;
   const int row = qt * 32 * WAVES + wave * 32 + col;
   const bool row_in = row < a.Q;
@@ -154,6 +182,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int n_tiles = range[0] >= 0 ? range[0] / NT + 1 : 0;
   // tiles below every valid row's remote limit: all keys remote, no masks
   const int full = range[1] == 0x7fffffff ? 0 : range[1] / NT;
+  // a long item runs as two pieces: tiles [0, half) and [half, n_tiles)
+  const bool split = n_tiles > a.q_split;
+  const int t0 = split && piece ? (n_tiles + 1) / 2 : 0;
+  const int t1 = split && !piece ? (n_tiles + 1) / 2 : n_tiles;
+  if (piece && !split) return;  // whole workgroup
 
   const T* kg = reinterpret_cast<const T*>(a.k) + ((int64_t)bi * N * H + hh) * D;
   const T* vg = reinterpret_cast<const T*>(a.v) + ((int64_t)bi * N * H + hh) * D;
@@ -163,7 +196,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     stager.template stage<NT>(BUF ? k1s : k0s, kg, kstride, i * NT, a.N);
     stager.template stage<NT>(BUF ? v1s : v0s, vg, kstride, i * NT, a.N);
   };
-  if (n_tiles > 0) stage.template operator()<0>(0);
+  if (t1 > t0) stage.template operator()<0>(t0);
 
   const int64_t obase = (((int64_t)bi * a.Q + (row_in ? row : 0)) * H + hh) * D;
   Frag qf[NKC], gf[NKC];
@@ -213,7 +246,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int kb = i * NT;
     wait_vm();
     __syncthreads();
-    if (i + 1 < n_tiles) stage.template operator()<1 - BUF>(i + 1);
+    if (i + 1 < t1) stage.template operator()<1 - BUF>(i + 1);
     const T* kt = BUF ? k1s : k0s;
     const T* vt = BUF ? v1s : v0s;
 
@@ -317,9 +350,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     if (i < full) step.template operator()<BUF, true>(i);
     else step.template operator()<BUF, false>(i);
   };
-  for (int i = 0; i < n_tiles; i += 2) {
+  for (int i = t0; i < t1; i += 2) {
     run.template operator()<0>(i);
-    if (i + 1 < n_tiles) run.template operator()<1>(i + 1);
+    if (i + 1 < t1) run.template operator()<1>(i + 1);
+  }
+  if (split) {
+    const int item = bh * n_qtiles + qt;
+    store_piece<NDT>(acc, a.q_part + (size_t)item * 2 * 4 * (NDT * 16 * 64), piece, a.q_count + item);
+    return;
   }
   if (!row_in) return;
   T* dq = reinterpret_cast<T*>(a.dq) + obase;
@@ -342,7 +380,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 // fragments stay in registers; dV^T += dO^T P and dK^T += Q^T dA take the
 // transposed operands from the staged tiles.
 template <typename T, int DP, int LOGB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void dense_bwd_dkv_fast_kernel(DenseArgs a, int n_rtiles) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void dense_bwd_dkv_fast_kernel(DenseArgs a, int n_rtiles, int n_ktiles) {
   typedef Mma<T> M;
   typedef typename M::Frag Frag;
   constexpr int WAVES = 4;
@@ -367,7 +405,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int col = lane & 31, half = lane >> 5;
   const int BH = a.B * a.H;
   const int bh = blockIdx.x % BH;
-  const int kt_idx = (int)(blockIdx.x / BH);  // ascending: the first key tiles see the most rows
+  // all first pieces, then all second pieces; ascending key tiles (the
+  // first key tiles see the most rows)
+  const int kk = (int)(blockIdx.x / BH);
+  const int piece = kk >= n_ktiles;
+  const int kt_idx = piece ? kk - n_ktiles : kk;
   const int bi = bh / a.H, hh = bh % a.H;
   const int kb = kt_idx * kKT;
   const int key = kb + 32 * wave + col;
@@ -408,6 +450,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
   __syncthreads();
   const int n_act = count;
+  // a long item runs as two pieces: row tiles [0, half) and [half, n_act)
+  const bool split = n_act > a.k_split;
+  const int i0 = split && piece ? (n_act + 1) / 2 : 0;
+  const int i1 = split && !piece ? (n_act + 1) / 2 : n_act;
+  if (piece && !split) return;  // whole workgroup
 
   const T* qg = reinterpret_cast<const T*>(a.q) + ((int64_t)bi * a.Q * H + hh) * D;
   const T* gg = reinterpret_cast<const T*>(a.dout) + ((int64_t)bi * a.Q * H + hh) * D;
@@ -429,7 +476,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
     if (threadIdx.x < 16) async_copy16(lg + m0 + 4 * threadIdx.x, BUF ? l1s : l0s);
   };
-  if (n_act > 0) stage.template operator()<0>(0);
+  if (i1 > i0) stage.template operator()<0>(i0);
 
   int qoff[NKC];
 #pragma unroll
@@ -465,7 +512,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   auto step = [&]<int BUF, bool FULL>(int idx) {
     wait_vm();
     __syncthreads();
-    if (idx + 1 < n_act) stage.template operator()<1 - BUF>(idx + 1);
+    if (idx + 1 < i1) stage.template operator()<1 - BUF>(idx + 1);
     const T* qt = BUF ? q1s : q0s;
     const T* gt = BUF ? g1s : g0s;
     const float* tt = reinterpret_cast<const float*>((BUF ? t1s : t0s) + tcol);
@@ -537,9 +584,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     if (list[idx] & 1) step.template operator()<BUF, true>(idx);
     else step.template operator()<BUF, false>(idx);
   };
-  for (int idx = 0; idx < n_act; idx += 2) {
+  for (int idx = i0; idx < i1; idx += 2) {
     run.template operator()<0>(idx);
-    if (idx + 1 < n_act) run.template operator()<1>(idx + 1);
+    if (idx + 1 < i1) run.template operator()<1>(idx + 1);
+  }
+  if (split) {
+    f32x16 both[2 * NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) { both[dt] = dk[dt]; both[NDT + dt] = dv[dt]; }
+    const int item = bh * n_ktiles + kt_idx;
+    store_piece<2 * NDT>(both, a.k_part + (size_t)item * 2 * 4 * (2 * NDT * 16 * 64), piece, a.k_count + item);
+    return;
   }
   if (key >= a.N) return;
   const int64_t kbase = (((int64_t)bi * N + key) * H + hh) * D;
@@ -561,22 +616,70 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
 }
 
+// ---------------------------------------------------------------------------
+// Sum of the two pieces of every split item: workgroup w < n_qitems handles
+// dQ item w (128 rows), the rest the dK/dV items (128 keys). Thread (wave,
+// lane) holds the registers of the same (wave, lane) of the piece kernels,
+// i.e. row/key 32*wave + lane%32 and dims 32*dt + 8*(r/4) + 4*(lane/32) + r%4.
+template <typename T, int DP>
+__global__ __launch_bounds__(256) void dense_bwd_merge_kernel(DenseArgs a, int n_qtiles, int n_ktiles) {
+  constexpr int NDT = DP / 32;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 31, half = lane >> 5;
+  const int BH = a.B * a.H;
+  const int n_qitems = BH * n_qtiles;
+  const bool is_q = (int)blockIdx.x < n_qitems;
+  const int item = is_q ? (int)blockIdx.x : (int)blockIdx.x - n_qitems;
+  if ((is_q ? a.q_count : a.k_count)[item] == 0) return;
+  const int n_t = is_q ? n_qtiles : n_ktiles;
+  const int bh = item / n_t, tile = item % n_t;
+  const int bi = bh / a.H, hh = bh % a.H;
+  const int idx = tile * 128 + wave * 32 + col;  // row (dQ) or key (dK/dV)
+  const int64_t H = a.H, D = a.D;
+  typedef T T4 __attribute__((ext_vector_type(4)));
+  const int nacc = is_q ? NDT : 2 * NDT;
+  const float* p0 = (is_q ? a.q_part : a.k_part) + ((size_t)item * 2 * 4 + wave) * (nacc * 16 * 64);
+  const float* p1 = p0 + (size_t)4 * nacc * 16 * 64;
+  if (idx >= (is_q ? a.Q : a.N)) return;
+  for (int t = 0; t < nacc; ++t) {
+    const int dt = t % NDT;
+    const float sc = (t < NDT) ? a.scale : 1.f;  // dQ and dK carry 1/sqrt(D); dV does not
+    T* dst;
+    if (is_q) dst = reinterpret_cast<T*>(a.dq) + (((int64_t)bi * a.Q + idx) * H + hh) * D;
+    else dst = reinterpret_cast<T*>(t < NDT ? a.dk : a.dv) + (((int64_t)bi * a.N + idx) * H + hh) * D;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      T4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = (t * 16 + 4 * i + j) * 64 + lane;
+        o[j] = from_float<T>((p0[r] + p1[r]) * sc);
+      }
+      *reinterpret_cast<T4*>(dst + 32 * dt + 8 * i + 4 * half) = o;
+    }
+  }
+}
+
 template <typename T, int DP>
 static hipError_t launch_fast(const DenseArgs& a, hipStream_t stream) {
   const int n_rows = a.B * a.Qp;
-  hipLaunchKernelGGL(dense_bwd_rows_kernel, dim3((n_rows + 255) / 256), dim3(256), 0, stream, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
   const int n_qtiles = (a.Q + 127) / 128;
   const int n_ktiles = (a.N + kKT - 1) / kKT;
   const int n_rtiles = a.Qp / kRT;
   const unsigned BH = (unsigned)(a.B * a.H);
+  hipLaunchKernelGGL(dense_bwd_rows_kernel, dim3((n_rows + 255) / 256), dim3(256), 0, stream, a,
+                     (int)(n_qtiles * BH), (int)(n_ktiles * BH));
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
   auto go = [&]<int LOGB>() {
-    hipLaunchKernelGGL((dense_bwd_dq_fast_kernel<T, DP, LOGB>), dim3(n_qtiles * BH), dim3(256), 0, stream, a,
-                       n_qtiles);
+    hipLaunchKernelGGL((dense_bwd_dq_fast_kernel<T, DP, LOGB>), dim3(2 * n_qtiles * BH), dim3(256), 0, stream,
+                       a, n_qtiles);
     if (hipPeekAtLastError() != hipSuccess) return;
-    hipLaunchKernelGGL((dense_bwd_dkv_fast_kernel<T, DP, LOGB>), dim3(n_ktiles * BH), dim3(256), 0, stream, a,
-                       n_rtiles);
+    hipLaunchKernelGGL((dense_bwd_dkv_fast_kernel<T, DP, LOGB>), dim3(2 * n_ktiles * BH), dim3(256), 0,
+                       stream, a, n_rtiles, n_ktiles);
+    if (hipPeekAtLastError() != hipSuccess) return;
+    hipLaunchKernelGGL((dense_bwd_merge_kernel<T, DP>), dim3((n_qtiles + n_ktiles) * BH), dim3(256), 0, stream,
+                       a, n_qtiles, n_ktiles);
   };
   switch (a.logb) {
     case 1: go.template operator()<1>(); break;

@@ -70,8 +70,12 @@ def test_argument_errors_map_to_value_error():
     # fp32: delta and rho only; bf16 head_dim 64: plus row limits, row-tile
     # statistics and the (beta, eps) table (B*H*Qp*nblk*8 bytes)
     assert lib.st_dense_bwd_workspace_bytes(0, 2, 5, 7, 3, 64, 4) == 2 * 256
-    # delta+rho 2*256, lim [2, 64] int32 512, tmin/tmax 2*256, table 2*3 heads x 32 blocks x 64 rows
-    assert lib.st_dense_bwd_workspace_bytes(2, 2, 5, 7, 3, 64, 4) == 2 * 256 + 512 + 2 * 256 + 2 * 3 * 32 * 64 * 8
+    # delta+rho 2*256, lim [2, 64] int32 512, tmin/tmax 2*256, table 2*3 heads x 32 blocks x 64 rows,
+    # two piece counters 2*256, dQ partials 6 items x 2 pieces x 128 x 64 floats, dK/dV twice that
+    table = 2 * 3 * 32 * 64 * 8
+    partials = 6 * 2 * 128 * 64 * 4 * 3
+    assert lib.st_dense_bwd_workspace_bytes(2, 2, 5, 7, 3, 64, 4) == (2 * 256 + 512 + 2 * 256 + table + 2 * 256
+                                                                       + partials)
     assert lib.st_dense_bwd_workspace_bytes(2, 2, 5, 7, 3, 64, 3) == 0
 
 
