@@ -617,8 +617,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 }
 
 // ---------------------------------------------------------------------------
-// Sum of the two pieces of every split item: workgroup w < n_qitems handles
-// dQ item w (128 rows), the rest the dK/dV items (128 keys). Thread (wave,
+// Sum of the two pieces of every split item: workgroup (w, t) with
+// w < n_qitems handles accumulator tile t of dQ item w (128 rows), the rest
+// the dK/dV items (128 keys; tiles 0..NDT-1 dK, NDT.. dV). Thread (wave,
 // lane) holds the registers of the same (wave, lane) of the piece kernels,
 // i.e. row/key 32*wave + lane%32 and dims 32*dt + 8*(r/4) + 4*(lane/32) + r%4.
 template <typename T, int DP>
@@ -641,7 +642,10 @@ __global__ __launch_bounds__(256) void dense_bwd_merge_kernel(DenseArgs a, int n
   const float* p0 = (is_q ? a.q_part : a.k_part) + ((size_t)item * 2 * 4 + wave) * (nacc * 16 * 64);
   const float* p1 = p0 + (size_t)4 * nacc * 16 * 64;
   if (idx >= (is_q ? a.Q : a.N)) return;
-  for (int t = 0; t < nacc; ++t) {
+  // one accumulator tile per workgroup (blockIdx.y): dQ has NDT, dK/dV 2*NDT
+  const int t = blockIdx.y;
+  if (t >= nacc) return;
+  {
     const int dt = t % NDT;
     const float sc = (t < NDT) ? a.scale : 1.f;  // dQ and dK carry 1/sqrt(D); dV does not
     T* dst;
@@ -678,8 +682,8 @@ static hipError_t launch_fast(const DenseArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL((dense_bwd_dkv_fast_kernel<T, DP, LOGB>), dim3(2 * n_ktiles * BH), dim3(256), 0,
                        stream, a, n_rtiles, n_ktiles);
     if (hipPeekAtLastError() != hipSuccess) return;
-    hipLaunchKernelGGL((dense_bwd_merge_kernel<T, DP>), dim3((n_qtiles + n_ktiles) * BH), dim3(256), 0, stream,
-                       a, n_qtiles, n_ktiles);
+    hipLaunchKernelGGL((dense_bwd_merge_kernel<T, DP>), dim3((n_qtiles + n_ktiles) * BH, 2 * (DP / 32)),
+                       dim3(256), 0, stream, a, n_qtiles, n_ktiles);
   };
   switch (a.logb) {
     case 1: go.template operator()<1>(); break;
