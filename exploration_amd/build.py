@@ -23,6 +23,9 @@ FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC",
     # no packed fp32 instructions anywhere in the device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # no NaN inputs are meaningful here: without IEEE mode, v_max/v_min need
+    # no canonicalising copy of each operand (one VALU op per max saved)
+    "-fno-honor-nans", "-mno-amdgpu-ieee",
     "-Wno-pass-failed",
 ]
 

@@ -28,6 +28,10 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kNegInf = -__builtin_inff();
+// Lazy online-softmax rescaling threshold (log2 units): the running row max
+// is only raised when a new score exceeds it by more than this, so the
+// exponentials of stale-max rows stay below 2^8 (far from fp32/bf16 overflow).
+constexpr float kLazyLog2 = 8.f;
 
 // Element-type traits: the MFMA used for this element type and how many
 // elements of an operand one lane holds per instruction.

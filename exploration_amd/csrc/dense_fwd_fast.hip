@@ -181,9 +181,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
       for (int r = 0; r < 16; r += 2) mt = fmaxf(mt, fmaxf(s[st][r], s[st][r + 1]));
     mt = fmaxf(mt, swap_halves(mt)) * a.scale_log2;
-    const float mn = fmaxf(m, mt);
-    const float msafe = mn == kNegInf ? 0.f : mn;
-    const float alpha = fast_exp2(m - msafe);
+    // Lazy rescaling: the running max m only moves when some row's tile max
+    // exceeds it by more than kLazyLog2 (so exponents stay below 2^kLazyLog2);
+    // otherwise alpha = 1 and the accumulator is left alone.
+    float alpha = 1.f;
+    if (__builtin_amdgcn_ballot_w64(mt > m + kLazyLog2)) {
+      const float mn = fmaxf(m, mt);
+      alpha = mn == kNegInf ? 0.f : fast_exp2(m - mn);
+      m = mn;
+      const float scale_acc = REMOTE ? alpha * alpha : alpha;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) acc[dt] *= scale_acc;
+    }
+    const float msafe = m == kNegInf ? 0.f : m;
     float psum = 0.f;
 #pragma unroll
     for (int st = 0; st < NST; ++st)
@@ -192,7 +202,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         s[st][r] = fast_exp2(fmaf(s[st][r], a.scale_log2, -msafe));
         psum += s[st][r];
       }
-    float scale_acc;
     zs = zs * alpha + psum;
     if constexpr (REMOTE) {
       float wsum;
@@ -214,16 +223,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             wsum += s[st][r];
           }
       }
-      scale_acc = alpha * alpha;
-      dr = dr * scale_acc + wsum;
-    } else {
-      scale_acc = alpha;
+      dr = dr * (alpha * alpha) + wsum;
     }
-    // unconditional: a wave-uniform skip branch costs more registers
-    // (spills) than the multiplies it saves
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) acc[dt] *= scale_acc;
-    m = mn;
     Frag bp[NST][2];
 #pragma unroll
     for (int st = 0; st < NST; ++st)
