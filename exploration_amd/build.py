@@ -30,13 +30,20 @@ FLAGS = [
 ]
 
 
+# Per-source extra flags. The pipelined forward keeps its score tiles in
+# VGPRs (MFMA results feed the softmax directly, no AGPR round trip).
+EXTRA_FLAGS = {
+    "dense_fwd_fast.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _sources():
     return sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
 def _digest(src):
     h = hashlib.sha256()
-    h.update(" ".join([HIPCC] + FLAGS).encode())
+    h.update(" ".join([HIPCC] + FLAGS + EXTRA_FLAGS.get(src, [])).encode())
     for name in sorted(os.listdir(CSRC)):
         if name.endswith(".h") or name == src:
             with open(os.path.join(CSRC, name), "rb") as f:
@@ -52,7 +59,7 @@ def _compile(src):
     if os.path.exists(obj):
         return obj
     tmp = obj + ".tmp"
-    cmd = [HIPCC] + FLAGS + ["-c", os.path.join(CSRC, src), "-o", tmp]
+    cmd = [HIPCC] + FLAGS + EXTRA_FLAGS.get(src, []) + ["-c", os.path.join(CSRC, src), "-o", tmp]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{proc.stderr}")

@@ -214,7 +214,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   int koff[NKC];
 #pragma unroll
   for (int c = 0; c < NKC; ++c) koff[c] = col * DP + (((2 * c + half) ^ swz<DP>(col)) * 8);
-  int toff[NDT];
+  int toff[NDT], toff8[NDT];  // rows r0 and r0 + 8 (swizzled separately)
   {
     const int gi = lane >> 4, sl = lane & 15;
     const int r0 = 4 * (gi >> 1) + (sl >> 2);
@@ -222,6 +222,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     for (int dt = 0; dt < NDT; ++dt) {
       const int d = 32 * dt + 16 * (gi & 1) + 4 * (sl & 3);
       toff[dt] = r0 * DP + (((d >> 3) ^ swz<DP>(r0)) * 8) + (d & 7);
+      toff8[dt] = (r0 + 8) * DP + (((d >> 3) ^ swz<DP>(r0 + 8)) * 8) + (d & 7);
     }
   }
   typedef short s4 __attribute__((ext_vector_type(4)));
@@ -231,8 +232,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   };
   auto tfrag = [&](const T* buf, int k0, int dt) -> Frag {
     const T* p0 = buf + k0 * DP + toff[dt];
+    const T* p1 = buf + k0 * DP + toff8[dt];
     s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)p0);
-    s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(p0 + 8 * DP));
+    s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)p1);
     return __builtin_bit_cast(Frag, (s8)__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   };
 
@@ -481,7 +483,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   int qoff[NKC];
 #pragma unroll
   for (int c = 0; c < NKC; ++c) qoff[c] = col * DP + (((2 * c + half) ^ swz<DP>(col)) * 8);
-  int toff[NDT];
+  int toff[NDT], toff8[NDT];  // rows r0 and r0 + 8 (swizzled separately)
   {
     const int gi = lane >> 4, sl = lane & 15;
     const int r0 = 4 * (gi >> 1) + (sl >> 2);
@@ -489,6 +491,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     for (int dt = 0; dt < NDT; ++dt) {
       const int d = 32 * dt + 16 * (gi & 1) + 4 * (sl & 3);
       toff[dt] = r0 * DP + (((d >> 3) ^ swz<DP>(r0)) * 8) + (d & 7);
+      toff8[dt] = (r0 + 8) * DP + (((d >> 3) ^ swz<DP>(r0 + 8)) * 8) + (d & 7);
     }
   }
   typedef short s4 __attribute__((ext_vector_type(4)));
@@ -498,8 +501,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   };
   auto tfrag = [&](const T* buf, int k0, int dt) -> Frag {
     const T* p0 = buf + k0 * DP + toff[dt];
+    const T* p1 = buf + k0 * DP + toff8[dt];
     s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)p0);
-    s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(p0 + 8 * DP));
+    s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)p1);
     return __builtin_bit_cast(Frag, (s8)__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   };
 

@@ -10,6 +10,8 @@
 //  * fixes the block size at compile time;
 //  * numbers workgroups head-fastest so consecutive workgroups, which the
 //    dispatcher spreads over the XCDs, keep one head's K/V per XCD L2.
+#include <utility>
+
 #include "dense.h"
 #include "tile.h"
 
@@ -72,12 +74,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const T* vg = reinterpret_cast<const T*>(a.v) + ((int64_t)bi * N * H + hh) * D;
   const int64_t kstride = H * D;
   const Stager<T, DP, WAVES> stager(kstride);
-  auto stage = [&]<int BUF>(int i) {
-    const int kb = tile_of(i) * NT;
-    stager.template stage<NT>(BUF ? k1s : k0s, kg, kstride, kb, a.N);
-    stager.template stage<NT>(BUF ? v1s : v0s, vg, kstride, kb, a.N);
-  };
-  if (total > 0) stage.template operator()<0>(0);
 
   Frag qf[NKC];
   {
@@ -92,7 +88,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   int koff[NKC];
 #pragma unroll
   for (int c = 0; c < NKC; ++c) koff[c] = col * DP + (((2 * c + half) ^ swz<DP>(col)) * 8);
-  int voff[NDT];
+  int voff[NDT], voff8[NDT];  // rows r0 and r0 + 8 (swizzled separately)
   {
     const int gi = lane >> 4, sl = lane & 15;
     const int r0 = 4 * (gi >> 1) + (sl >> 2);
@@ -100,6 +96,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     for (int dt = 0; dt < NDT; ++dt) {
       const int d = 32 * dt + 16 * (gi & 1) + 4 * (sl & 3);
       voff[dt] = r0 * DP + (((d >> 3) ^ swz<DP>(r0)) * 8) + (d & 7);
+      voff8[dt] = (r0 + 8) * DP + (((d >> 3) ^ swz<DP>(r0 + 8)) * 8) + (d & 7);
     }
   }
   typedef short s4 __attribute__((ext_vector_type(4)));
@@ -109,23 +106,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   };
   auto vfrag = [&](const T* buf, int k0, int dt) -> Frag {
     const T* p0 = buf + k0 * DP + voff[dt];
+    const T* p1 = buf + k0 * DP + voff8[dt];
     s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)p0);
-    s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(p0 + 8 * DP));
+    s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)p1);
     return __builtin_bit_cast(Frag, (s8)__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   };
 
   f32x16 acc[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) acc[dt] = zero16();
-  float m = kNegInf, zs = 0.f, dr = 0.f;
+  // running state of the remote pass (max, row sum, sum of squared block
+  // sums) and of the local pass (max, row sum); maxima in log2 units
+  float m_r = kNegInf, zs_r = 0.f, dr = 0.f, m_l = kNegInf, zs_l = 0.f;
   float log_zr = kNegInf, lr = kNegInf;
   const int64_t obase = (((int64_t)bi * a.Q + row) * H + hh) * D;
 
   auto finish_remote = [&]() {
-    zs += swap_halves(zs);
+    zs_r += swap_halves(zs_r);
     dr += swap_halves(dr);
-    log_zr = log_mass(m, zs);
-    lr = dr > 0.f ? log_mass(m, dr) - fast_log2(zs) * kLn2 : kNegInf;
+    log_zr = log_mass(m_r, zs_r);
+    lr = dr > 0.f ? log_mass(m_r, dr) - fast_log2(zs_r) * kLn2 : kNegInf;
     const float inv = dr > 0.f ? 1.f / dr : 0.f;
     if (row_in) {
 #pragma unroll
@@ -140,119 +140,220 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) acc[dt] = zero16();
-    m = kNegInf;
-    zs = 0.f;  // reused as the local denominator
   };
 
-  auto step = [&]<int BUF, bool REMOTE, bool MASKED>(int i) {
-    if (i == n_remote) finish_remote();
-    const int kb = tile_of(i) * NT;
-    wait_vm();
-    __syncthreads();
-    if (i + 1 < total) stage.template operator()<1 - BUF>(i + 1);
-    const T* kt = BUF ? k1s : k0s;
-    const T* vt = BUF ? v1s : v0s;
+  // Software pipeline over the tile sequence. Iteration i issues, in one
+  // scheduling region, the PV MFMAs of tile i-1 (V buffer (i+1)&1) while the
+  // VALU masks, maximises and exponentiates the scores of tile i, then the
+  // S^T MFMAs of tile i+1 (K buffer (i+1)&1) while the VALU scales and
+  // converts tile i to 16-bit probabilities; the S^T products of subtile st
+  // overwrite scores the softmax has finished with, so one score buffer and
+  // one probability buffer suffice. Products go in chunks of 4 with their LDS
+  // reads one chunk ahead. Past the ends of the sequence the MFMAs run on
+  // finite filler data whose results are never used (probabilities of tile
+  // -1 are zero; scores of tile `total` are discarded).
+  f32x16 sc[NST];
+  Frag pf[NST][2];
+#pragma unroll
+  for (int st = 0; st < NST; ++st)
+#pragma unroll
+    for (int c2 = 0; c2 < 2; ++c2) pf[st][c2] = Frag{};
+  constexpr int NSP = NST * NKC;      // S^T products per tile
+  constexpr int NPV = NST * 2 * NDT;  // PV products per tile
+  constexpr int H1 = NPV / 4;         // chunks of the first half (PV)
+  constexpr int H2 = NSP / 4;         // chunks of the second half (S^T)
+  constexpr int CPS = H2 / NST;       // chunks per score subtile
+  static_assert(NPV % 4 == 0 && NSP % 4 == 0 && H2 % NST == 0, "chunks of 4 products");
+  constexpr int NSL1 = 10;            // first-half softmax slices
 
-    f32x16 s[NST];
+  float mt = kNegInf, msafe = 0.f, alpha = 1.f, psum = 0.f, blk1 = 0.f;
+  bool grow = false;
+  float blkv[NST][8];
+  // First-half slice K: masks and row max (K < 2), exponentials (K >= 2).
+  auto slice1 = [&]<int K, bool MASKED>(bool remote, int kb) {
+    if constexpr (K < 2) {
+      constexpr int s0 = K * ((NST + 1) / 2);
+      constexpr int s1 = K ? NST : (NST + 1) / 2;
+      if constexpr (MASKED) {
+        // key of register r in subtile st is kb + 4*half + (32*st + 8*(r/4) + r%4)
+        const int base = kb + 4 * half;
+        const int lim = (remote ? rlim : lhi + 1) - base;
+        const int lo = remote ? INT32_MIN : llo - base;
 #pragma unroll
-    for (int st = 0; st < NST; ++st) s[st] = zero16();
-    // product j: subtile j / NKC, contraction chunk j % NKC
-    mfma_phase<NST * NKC, 4, 1>([&](int j) { return kfrag(kt, j / NKC, j % NKC); },
-                             [&](int j, Frag f) { s[j / NKC] = M::mma(f, qf[j % NKC], s[j / NKC]); });
-    // Raw dot products; the scale is applied inside exp2(s*c - m).
-    if constexpr (MASKED) {
-      // key of register r in subtile st is kb + 4*half + (32*st + 8*(r/4) + r%4):
-      // compare the compile-time offset against per-lane thresholds
-      const int base = kb + 4 * half;
-      const int lim = (REMOTE ? rlim : lhi + 1) - base;
-      const int lo = REMOTE ? INT32_MIN : llo - base;
-#pragma unroll
-      for (int st = 0; st < NST; ++st)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          constexpr int dummy = 0;
-          const int off = 32 * st + 8 * (r >> 2) + (r & 3) + dummy;
-          s[st][r] = ((off < lim) & (off >= lo)) ? s[st][r] : kNegInf;
-        }
-    }
-    float mt = kNegInf;
-#pragma unroll
-    for (int st = 0; st < NST; ++st)
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) mt = fmaxf(mt, fmaxf(s[st][r], s[st][r + 1]));
-    mt = fmaxf(mt, swap_halves(mt)) * a.scale_log2;
-    // Lazy rescaling: the running max m only moves when some row's tile max
-    // exceeds it by more than kLazyLog2 (so exponents stay below 2^kLazyLog2);
-    // otherwise alpha = 1 and the accumulator is left alone.
-    float alpha = 1.f;
-    if (__builtin_amdgcn_ballot_w64(mt > m + kLazyLog2)) {
-      const float mn = fmaxf(m, mt);
-      alpha = mn == kNegInf ? 0.f : fast_exp2(m - mn);
-      m = mn;
-      const float scale_acc = REMOTE ? alpha * alpha : alpha;
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) acc[dt] *= scale_acc;
-    }
-    const float msafe = m == kNegInf ? 0.f : m;
-    float psum = 0.f;
-#pragma unroll
-    for (int st = 0; st < NST; ++st)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[st][r] = fast_exp2(fmaf(s[st][r], a.scale_log2, -msafe));
-        psum += s[st][r];
-      }
-    zs = zs * alpha + psum;
-    if constexpr (REMOTE) {
-      float wsum;
-      if constexpr ((1 << LOGB) == NT) {
-        // the tile is one block: its row sum is the block sum
-        const float blk = psum + swap_halves(psum);
-#pragma unroll
-        for (int st = 0; st < NST; ++st) s[st] *= blk;
-        wsum = psum * blk;
-      } else {
-        float blk[NST][8];
-        block_sums<NST, LOGB>(s, blk);
-        wsum = 0.f;
-#pragma unroll
-        for (int st = 0; st < NST; ++st)
+        for (int st = s0; st < s1; ++st)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            s[st][r] *= blk[st][blk_slot<LOGB>(r)];
-            wsum += s[st][r];
+            const int off = 32 * st + 8 * (r >> 2) + (r & 3);
+            sc[st][r] = ((off < lim) & (off >= lo)) ? sc[st][r] : kNegInf;
           }
       }
-      dr = dr * (alpha * alpha) + wsum;
+#pragma unroll
+      for (int st = s0; st < s1; ++st)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) mt = fmaxf(mt, fmaxf(sc[st][r], sc[st][r + 1]));
+      if constexpr (K == 1) {
+        mt = fmaxf(mt, swap_halves(mt)) * a.scale_log2;
+        // lazy rescaling: the max only moves when some row of the wave
+        // exceeds it by more than kLazyLog2 (alpha is exactly 1 otherwise)
+        const float m = remote ? m_r : m_l;
+        grow = __builtin_amdgcn_ballot_w64(mt > m + kLazyLog2) != 0;
+        const float mn = grow ? fmaxf(m, mt) : m;
+        msafe = mn == kNegInf ? 0.f : mn;
+        alpha = fast_exp2(m - msafe);
+        if (remote) m_r = mn;
+        else m_l = mn;
+        mt = kNegInf;
+        psum = 0.f;
+      }
+    } else {
+      constexpr int v0 = (16 * NST) * (K - 2) / 8, v1 = (16 * NST) * (K - 1) / 8;
+#pragma unroll
+      for (int v = v0; v < v1; ++v) {
+        const float x = fast_exp2(fmaf(sc[v / 16][v % 16], a.scale_log2, -msafe));
+        sc[v / 16][v % 16] = x;
+        psum += x;
+      }
     }
-    Frag bp[NST][2];
+  };
+  // Second-half slice for score subtile ST: the block scaling (remote pass)
+  // and the conversion to 16-bit probabilities, after which sc[ST] is free.
+  auto slice2 = [&]<int ST>(bool remote) {
+    if constexpr (ST == 0) {
+      if (remote) zs_r = zs_r * alpha + psum;
+      else zs_l = zs_l * alpha + psum;
+      if (remote) {
+        if constexpr ((1 << LOGB) == NT) {
+          // the tile is one block: its row sum is the block sum
+          blk1 = psum + swap_halves(psum);
+          dr = dr * (alpha * alpha) + psum * blk1;
+        } else {
+          block_sums<NST, LOGB>(sc, blkv);
+          dr *= alpha * alpha;
+        }
+      }
+    }
+    if (remote) {
+      if constexpr ((1 << LOGB) == NT) {
+        sc[ST] *= blk1;
+      } else {
+        float w = 0.f;
 #pragma unroll
-    for (int st = 0; st < NST; ++st)
+        for (int r = 0; r < 16; ++r) {
+          sc[ST][r] *= blkv[ST][blk_slot<LOGB>(r)];
+          w += sc[ST][r];
+        }
+        dr += w;
+      }
+    }
 #pragma unroll
-      for (int c2 = 0; c2 < 2; ++c2) bp[st][c2] = frag_from_c<T>(s[st], c2);
-    // product j: 16-key chunk j / NDT, head-dim tile j % NDT
+    for (int c2 = 0; c2 < 2; ++c2) pf[ST][c2] = frag_from_c<T>(sc[ST], c2);
+  };
+
+  // MASKED = false: an unmasked remote tile (the bulk); MASKED = true: any
+  // tile, remote or local, with the causal / window masks applied.
+  auto iteration = [&]<int PAR, bool MASKED>(int i) {
+    const bool remote = MASKED ? i < n_remote : true;
+    wait_vm();
+    __syncthreads();
+    if (i + 2 < total) stager.template stage<NT>(PAR ? k1s : k0s, kg, kstride, tile_of(i + 2) * NT, a.N);
+    stager.template stage<NT>(PAR ? v1s : v0s, vg, kstride, tile_of(i) * NT, a.N);
+    const T* kt = PAR ? k0s : k1s;
+    const T* vt = PAR ? v0s : v1s;
+    const int kb = tile_of(i) * NT;
+    // chunk g < H1: PV products 4g..4g+3 (head-dim tile q % NDT, 16-key chunk
+    // q / NDT); chunk H1 + h: S^T subtile h / CPS, contraction chunks
+    // 4 (h % CPS) .. +3
+    auto load = [&](int g, int u) -> Frag {
+      if (g < H1) {
+        const int q = 4 * g + u;
+        return vfrag(vt, 16 * (q / NDT), q % NDT);
+      }
+      const int h = g - H1;
+      return kfrag(kt, h / CPS, 4 * (h % CPS) + u);
+    };
+    Frag buf[2][4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) buf[0][u] = load(0, u);
+    [&]<int... G>(std::integer_sequence<int, G...>) {
+      ([&] {
+        constexpr int g = G;
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this chunk's reads
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (g + 1 < H1 + H2) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) buf[(g + 1) & 1][u] = load(g + 1, u);
+        }
+        if constexpr (g < H1) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int q = 4 * g + u;
+            acc[q % NDT] = M::mma(buf[g & 1][u], pf[q / (2 * NDT)][(q / NDT) & 1], acc[q % NDT]);
+          }
+          [&]<int... L>(std::integer_sequence<int, L...>) {
+            (slice1.template operator()<g * NSL1 / H1 + L, MASKED>(remote, kb), ...);
+          }(std::make_integer_sequence<int, (g + 1) * NSL1 / H1 - g * NSL1 / H1>{});
+        } else {
+          constexpr int h = g - H1, st = h / CPS;
+          if constexpr (h % CPS == 0) slice2.template operator()<st>(remote);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int c = 4 * (h % CPS) + u;
+            sc[st] = M::mma(buf[g & 1][u], qf[c], c == 0 ? zero16() : sc[st]);
+          }
+        }
+      }(), ...);
+    }(std::make_integer_sequence<int, H1 + H2>{});
+    __builtin_amdgcn_sched_barrier(0);
+    if (i == n_remote) {
+      finish_remote();
+    } else if (grow) {
+      const float f = remote ? alpha * alpha : alpha;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) acc[dt] *= f;
+    }
+  };
+
+  if (total > 0) {
+    // prologue: K of tiles 0 and 1, finite filler in the V buffer iteration 0
+    // reads, then the S^T products of tile 0
+    stager.template stage<NT>(k0s, kg, kstride, tile_of(0) * NT, a.N);
+    stager.template stage<NT>(v1s, vg, kstride, tile_of(0) * NT, a.N);
+    if (total > 1) stager.template stage<NT>(k1s, kg, kstride, tile_of(1) * NT, a.N);
+    wait_vm();
+    __syncthreads();
+#pragma unroll
+    for (int st = 0; st < NST; ++st) sc[st] = zero16();
+    mfma_phase<NST * NKC, 4, 1>([&](int j) { return kfrag(k0s, j / NKC, j % NKC); },
+                                [&](int j, Frag f) { sc[j / NKC] = M::mma(f, qf[j % NKC], sc[j / NKC]); });
+  }
+  // unmasked remote tiles in pairs (an even count; an odd last one joins the
+  // masked loop), then every remaining tile through the masked variant
+  const int n_fast = (full_remote < n_remote ? full_remote : n_remote) & ~1;
+  int i = 0;
+  for (; i < n_fast; i += 2) {
+    iteration.template operator()<0, false>(i);
+    iteration.template operator()<1, false>(i + 1);
+  }
+  for (; i < total; i += 2) {
+    iteration.template operator()<0, true>(i);
+    if (i + 1 < total) iteration.template operator()<1, true>(i + 1);
+  }
+  if (total > 0) {
+    // drain: PV products of the last tile
+    wait_vm();
+    __syncthreads();
+    const T* vt = (total - 1) & 1 ? v1s : v0s;
     mfma_phase<NST * 2 * NDT, 4, 2>(
         [&](int j) { return vfrag(vt, 16 * (j / NDT), j % NDT); },
-        [&](int j, Frag f) { acc[j % NDT] = M::mma(f, bp[j / (2 * NDT)][(j / NDT) & 1], acc[j % NDT]); });
-  };
-  auto run = [&]<int BUF>(int i) {
-    if (i < n_remote) {
-      if (tile_of(i) < full_remote) step.template operator()<BUF, true, false>(i);
-      else step.template operator()<BUF, true, true>(i);
-    } else {
-      step.template operator()<BUF, false, true>(i);
-    }
-  };
-  for (int i = 0; i < total; i += 2) {
-    run.template operator()<0>(i);
-    if (i + 1 < total) run.template operator()<1>(i + 1);
+        [&](int j, Frag f) { acc[j % NDT] = M::mma(f, pf[j / (2 * NDT)][(j / NDT) & 1], acc[j % NDT]); });
   }
   if (total == n_remote) finish_remote();
   // local statistics (zs now holds the local denominator); padding rows,
   // which skipped masks on full remote tiles, have no mass at all
-  const float zsum = zs + swap_halves(zs);
+  const float zsum = zs_l + swap_halves(zs_l);
   const float dl = p >= 0 ? zsum : 0.f;
-  const float ll = p >= 0 ? log_mass(m, dl) : kNegInf;
+  const float ll = p >= 0 ? log_mass(m_l, dl) : kNegInf;
   if (p < 0) {
     lr = kNegInf;
     log_zr = kNegInf;
