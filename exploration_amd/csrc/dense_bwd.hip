@@ -179,7 +179,7 @@ __global__ __launch_bounds__(WAVES * 64) void dense_bwd_dq_kernel(DenseArgs a) {
   T* lds_k = lds_buf;
   T* lds_v = SEQ ? lds_buf : lds_buf + ROW_ELEMS;
   T* lds_kt = SEQ ? lds_buf : lds_buf + 2 * ROW_ELEMS;
-  __shared__ int range;
+  __shared__ int range[WAVES];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 31, half = lane >> 5;
@@ -190,11 +190,15 @@ __global__ __launch_bounds__(WAVES * 64) void dense_bwd_dq_kernel(DenseArgs a) {
   const int64_t H = a.H, D = a.D, N = a.N;
   const RowStats rs = row_stats(a, bi, row, hh);
 
-  if (threadIdx.x == 0) range = -1;
+  {
+    const int r0 = wave_max(rs.lhi >= 0 ? rs.lhi : -1);
+    if (lane == 0) range[wave] = r0;
+  }
   __syncthreads();
-  if (rs.lhi >= 0) atomicMax(&range, rs.lhi);
-  __syncthreads();
-  const int n_tiles = range >= 0 ? range / NT + 1 : 0;
+  int rg = range[0];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) rg = max(rg, range[w]);
+  const int n_tiles = rg >= 0 ? rg / NT + 1 : 0;
 
   const T* kg = reinterpret_cast<const T*>(a.k) + ((int64_t)bi * N * H + hh) * D;
   const T* vg = reinterpret_cast<const T*>(a.v) + ((int64_t)bi * N * H + hh) * D;

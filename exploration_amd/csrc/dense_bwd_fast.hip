@@ -140,7 +140,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   __shared__ __attribute__((aligned(16))) T k1s[TILE];
   __shared__ __attribute__((aligned(16))) T v0s[TILE];
   __shared__ __attribute__((aligned(16))) T v1s[TILE];
-  __shared__ int range[2];
+  __shared__ int range[2][WAVES];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 31, half = lane >> 5;
@@ -175,13 +175,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     dl = a.delta[sidx];
     rho = a.rho[sidx];
   }
-  if (threadIdx.x == 0) { range[0] = -1; range[1] = 0x7fffffff; }
+  {
+    const int r0 = wave_max(lhi), r1 = wave_min(lhi >= 0 ? rlim : 0x7fffffff);
+    if (lane == 0) { range[0][wave] = r0; range[1][wave] = r1; }
+  }
   __syncthreads();
-  if (lhi >= 0) { atomicMax(&range[0], lhi); atomicMin(&range[1], rlim); }
-  __syncthreads();
-  const int n_tiles = range[0] >= 0 ? range[0] / NT + 1 : 0;
+  int rg0 = range[0][0], rg1 = range[1][0];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) { rg0 = max(rg0, range[0][w]); rg1 = min(rg1, range[1][w]); }
+  const int n_tiles = rg0 >= 0 ? rg0 / NT + 1 : 0;
   // tiles below every valid row's remote limit: all keys remote, no masks
-  const int full = range[1] == 0x7fffffff ? 0 : range[1] / NT;
+  const int full = rg1 == 0x7fffffff ? 0 : rg1 / NT;
   // a long item runs as two pieces: tiles [0, half) and [half, n_tiles)
   const bool split = n_tiles > a.q_split;
   const int t0 = split && piece ? (n_tiles + 1) / 2 : 0;

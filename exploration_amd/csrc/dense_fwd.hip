@@ -38,7 +38,7 @@ __global__ __launch_bounds__(WAVES * 64) void dense_fwd_kernel(DenseArgs a) {
                                                            : KBYTES / sizeof(T)];
   __shared__ __attribute__((aligned(16))) T lds_v_own[SHARED ? 1 : VBYTES / sizeof(T)];
   T* lds_v = SHARED ? lds_k : lds_v_own;
-  __shared__ int range[3];
+  __shared__ int range[3][WAVES];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 31, half = lane >> 5;
@@ -59,14 +59,22 @@ __global__ __launch_bounds__(WAVES * 64) void dense_fwd_kernel(DenseArgs a) {
     llo = (int)lo;
     lhi = (int)(p < N - 1 ? p : N - 1);
   }
-  if (threadIdx.x == 0) { range[0] = 0; range[1] = 0x7fffffff; range[2] = -1; }
+  {
+    const bool win = lhi >= llo;
+    const int r0 = wave_max(rlim), r1 = wave_min(win ? llo : 0x7fffffff), r2 = wave_max(win ? lhi : -1);
+    if (lane == 0) { range[0][wave] = r0; range[1][wave] = r1; range[2][wave] = r2; }
+  }
   __syncthreads();
-  atomicMax(&range[0], rlim);
-  if (lhi >= llo) { atomicMin(&range[1], llo); atomicMax(&range[2], lhi); }
-  __syncthreads();
-  const int n_remote_tiles = (range[0] + NT - 1) / NT;
-  const int lt0 = range[2] >= 0 ? range[1] / NT : 0;
-  const int lt1 = range[2] >= 0 ? range[2] / NT : -1;
+  int rg0 = range[0][0], rg1 = range[1][0], rg2 = range[2][0];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) {
+    rg0 = max(rg0, range[0][w]);
+    rg1 = min(rg1, range[1][w]);
+    rg2 = max(rg2, range[2][w]);
+  }
+  const int n_remote_tiles = (rg0 + NT - 1) / NT;
+  const int lt0 = rg2 >= 0 ? rg1 / NT : 0;
+  const int lt1 = rg2 >= 0 ? rg2 / NT : -1;
 
   const T* qg = reinterpret_cast<const T*>(a.q);
   const T* kg = reinterpret_cast<const T*>(a.k) + ((int64_t)bi * N * H + hh) * D;

@@ -34,7 +34,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   __shared__ __attribute__((aligned(16))) T k1s[TILE];
   __shared__ __attribute__((aligned(16))) T v0s[TILE];
   __shared__ __attribute__((aligned(16))) T v1s[TILE];
-  __shared__ int range[4];
+  __shared__ int range[4][WAVES];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 31, half = lane >> 5;
@@ -56,17 +56,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     llo = (int)lo;
     lhi = (int)(p < N - 1 ? p : N - 1);
   }
-  if (threadIdx.x == 0) { range[0] = 0; range[1] = 0x7fffffff; range[2] = -1; range[3] = 0x7fffffff; }
+  // workgroup ranges: max remote limit, min / max local key, min remote
+  // limit of the rows with a local window
+  {
+    const bool win = lhi >= llo;
+    const int r0 = wave_max(rlim), r1 = wave_min(win ? llo : 0x7fffffff);
+    const int r2 = wave_max(win ? lhi : -1), r3 = wave_min(win ? rlim : 0x7fffffff);
+    if (lane == 0) { range[0][wave] = r0; range[1][wave] = r1; range[2][wave] = r2; range[3][wave] = r3; }
+  }
   __syncthreads();
-  atomicMax(&range[0], rlim);
-  if (lhi >= llo) { atomicMin(&range[1], llo); atomicMax(&range[2], lhi); atomicMin(&range[3], rlim); }
-  __syncthreads();
+  int rg0 = range[0][0], rg1 = range[1][0], rg2 = range[2][0], rg3 = range[3][0];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) {
+    rg0 = max(rg0, range[0][w]);
+    rg1 = min(rg1, range[1][w]);
+    rg2 = max(rg2, range[2][w]);
+    rg3 = min(rg3, range[3][w]);
+  }
   // remote tiles ending at or below every valid row's remote limit need no
   // masks (padding rows are zeroed when the row is finalised)
-  const int full_remote = range[3] == 0x7fffffff ? 0 : range[3] / NT;
-  const int n_remote = (range[0] + NT - 1) / NT;
-  const int lt0 = range[2] >= 0 ? range[1] / NT : 0;
-  const int n_local = range[2] >= 0 ? range[2] / NT - lt0 + 1 : 0;
+  const int full_remote = rg3 == 0x7fffffff ? 0 : rg3 / NT;
+  const int n_remote = (rg0 + NT - 1) / NT;
+  const int lt0 = rg2 >= 0 ? rg1 / NT : 0;
+  const int n_local = rg2 >= 0 ? rg2 / NT - lt0 + 1 : 0;
   const int total = n_remote + n_local;
   auto tile_of = [&](int i) { return i < n_remote ? i : lt0 + (i - n_remote); };
 
@@ -112,15 +124,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     return __builtin_bit_cast(Frag, (s8)__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   };
 
+  // PV accumulator (acc^T[d][row], lane = row): the remote pass, then the
+  // local pass
   f32x16 acc[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) acc[dt] = zero16();
+  const int64_t obase = (((int64_t)bi * a.Q + row) * H + hh) * D;
   // running state of the remote pass (max, row sum, sum of squared block
   // sums) and of the local pass (max, row sum); maxima in log2 units
   float m_r = kNegInf, zs_r = 0.f, dr = 0.f, m_l = kNegInf, zs_l = 0.f;
   float log_zr = kNegInf, lr = kNegInf;
-  const int64_t obase = (((int64_t)bi * a.Q + row) * H + hh) * D;
 
+  // End of the remote pass: its statistics, and its mean parked in rc (one
+  // burst of stores that drains while the local tiles run; registers cannot
+  // hold two accumulators next to the pipelined loop).
   auto finish_remote = [&]() {
     zs_r += swap_halves(zs_r);
     dr += swap_halves(dr);
@@ -305,6 +322,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       }(), ...);
     }(std::make_integer_sequence<int, H1 + H2>{});
     __builtin_amdgcn_sched_barrier(0);
+    // the last remote PV products (tile i-1) are in: park the remote pass;
+    // otherwise a raised max rescales the accumulator before the PV products
+    // of tile i (next iteration)
     if (i == n_remote) {
       finish_remote();
     } else if (grow) {
@@ -362,31 +382,68 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const float safe_total = tot == kNegInf ? 0.f : tot;
   const float prem = lr == kNegInf ? 0.f : __expf(lr - safe_total);
   const float ploc = ll == kNegInf ? 0.f : __expf(ll - safe_total);
-  if (!row_in) return;
   const float linv = dl > 0.f ? ploc / dl : 0.f;
-  T* og = reinterpret_cast<T*>(a.out);
+  if (half == 0 && row_in) {
+    const int64_t sidx = ((int64_t)bi * a.Q + row) * H + hh;
+    a.pr[sidx] = prem;
+    a.zr[sidx] = log_zr;
+    a.z[sidx] = tot;
+  }
+  // rc = prem * (parked remote mean) and out = rc + ploc * (local mean), in
+  // row-contiguous form: each wave stages its 32 rows' local part and weights
+  // in one 32 KiB K/V buffer (free after the drain) and then reads, combines
+  // and writes whole rows. With lane = row, direct global accesses would
+  // touch 64 cache lines per instruction.
+  constexpr int RLD = DP + 4;  // fp32 staging stride: conflict-free 16-byte writes
+  static_assert(32 * RLD * 4 + 32 * 4 <= TILE * (int)sizeof(T), "staging fits one buffer");
+  __syncthreads();  // every wave is done with the K/V buffers
+  float* lst = reinterpret_cast<float*>(wave == 0 ? k0s : (wave == 1 ? k1s : (wave == 2 ? v0s : v1s)));
+  float* wst = lst + 32 * RLD;  // per-row prem
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int d = 32 * dt + 8 * i + 4 * half;
-      f32x4 rv = *reinterpret_cast<const f32x4*>(a.rc + obase + d);
-      f32x4 rc;
-      typedef T T4 __attribute__((ext_vector_type(4)));
-      T4 o;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        rc[j] = rv[j] * prem;
-        o[j] = from_float<T>(rc[j] + acc[dt][4 * i + j] * linv);
-      }
-      *reinterpret_cast<f32x4*>(a.rc + obase + d) = rc;
-      *reinterpret_cast<T4*>(og + obase + d) = o;
+      const f32x4 lv = {acc[dt][4 * i] * linv, acc[dt][4 * i + 1] * linv, acc[dt][4 * i + 2] * linv,
+                        acc[dt][4 * i + 3] * linv};
+      *reinterpret_cast<f32x4*>(lst + col * RLD + d) = lv;
     }
-  if (half == 0) {
-    const int64_t sidx = ((int64_t)bi * a.Q + row) * H + hh;
-    a.pr[sidx] = prem;
-    a.zr[sidx] = log_zr;
-    a.z[sidx] = tot;
+  if (half == 0) wst[col] = prem;
+  // the parked rc stores of this wave are visible to all its lanes
+  __threadfence_block();
+  __syncthreads();
+  {
+    constexpr int RL = DP / 4;  // lanes per row, 4 floats each
+    const int row0 = qt * 32 * WAVES + wave * 32;
+    typedef T T4 __attribute__((ext_vector_type(4)));
+    constexpr int NIT = 32 * RL / 64;
+    // every load before the first store (the stores may alias in the
+    // compiler's view, which would serialise the round trips)
+    f32x4 mean[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const int r = (it * 64 + lane) / RL, c = ((it * 64 + lane) % RL) * 4;
+      const int64_t g = (((int64_t)bi * a.Q + row0 + r) * H + hh) * D + c;
+      mean[it] = row0 + r < a.Q ? *reinterpret_cast<const f32x4*>(a.rc + g) : f32x4{};
+    }
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const int r = (it * 64 + lane) / RL, c = ((it * 64 + lane) % RL) * 4;
+      if (row0 + r < a.Q) {
+        const int64_t g = (((int64_t)bi * a.Q + row0 + r) * H + hh) * D + c;
+        const float w = wst[r];
+        const f32x4 lv = *reinterpret_cast<const f32x4*>(lst + r * RLD + c);
+        f32x4 rc;
+        T4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          rc[j] = mean[it][j] * w;
+          o[j] = from_float<T>(rc[j] + lv[j]);
+        }
+        *reinterpret_cast<f32x4*>(a.rc + g) = rc;
+        *reinterpret_cast<T4*>(reinterpret_cast<T*>(a.out) + g) = o;
+      }
+    }
   }
 }
 
