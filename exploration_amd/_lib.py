@@ -23,7 +23,9 @@ SIGNATURES = {
     "st_abi_version": (ctypes.c_int, []),
     "st_last_error": (ctypes.c_char_p, []),
     "st_dense_supported": (ctypes.c_int, [ctypes.c_int, _i64, _i64]),
-    "st_dense_fwd": (ctypes.c_int, [ctypes.c_int] + [_i64] * 6 + [_p] * 3 + [_i64p, _p] + [_f32p] * 4 + [_p]),
+    "st_dense_fwd_workspace_bytes": (_sz, [ctypes.c_int] + [_i64] * 6),
+    "st_dense_fwd": (ctypes.c_int, [ctypes.c_int] + [_i64] * 6 + [_p] * 3 + [_i64p, _p] + [_f32p] * 4
+                     + [_p, _sz, _p]),
     "st_dense_bwd_workspace_bytes": (_sz, [ctypes.c_int] + [_i64] * 6),
     "st_dense_bwd": (ctypes.c_int, [ctypes.c_int] + [_i64] * 6 + [_p] * 3 + [_i64p, _p] + [_f32p] * 4
                      + [_p] * 4 + [_p, _sz, _p]),
@@ -37,7 +39,7 @@ SIGNATURES = {
                       + [_p, _i64p, _f32p, _f32p, _f32p, _p, _sz, _p]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 _lib = None
 
 

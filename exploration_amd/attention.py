@@ -74,10 +74,12 @@ class _DenseHip(torch.autograd.Function):
         pr = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
         zr, z = torch.empty_like(pr), torch.empty_like(pr)
         code = _lib.DTYPE_CODES[q.dtype]
+        ws_bytes = lib.st_dense_fwd_workspace_bytes(code, batch, queries, keys, heads, dim, block_size)
+        ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8) if ws_bytes else None
         _lib.check(lib.st_dense_fwd(code, batch, queries, keys, heads, dim, block_size,
                                     _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(positions),
                                     _lib.ptr(out), _lib.ptr(rc), _lib.ptr(pr), _lib.ptr(zr), _lib.ptr(z),
-                                    _lib.stream_of(q)), lib)
+                                    _lib.ptr(ws), ws_bytes, _lib.stream_of(q)), lib)
         _record("dense_fwd", q, block_size)
         ctx.save_for_backward(q, k, v, positions, out, rc, pr, zr, z)
         ctx.block_size = block_size

@@ -88,19 +88,41 @@ int st_dense_supported(int dtype, int64_t head_dim, int64_t block_size) {
   return check_envelope(head_dim, block_size) == ST_OK ? 1 : 0;
 }
 
+size_t st_dense_fwd_workspace_bytes(int dtype, int64_t batch, int64_t queries, int64_t keys,
+                                    int64_t heads, int64_t head_dim, int64_t block_size) {
+  if (check_dtype(dtype) || check_sizes(batch, queries, keys, heads, head_dim, block_size) ||
+      check_envelope(head_dim, block_size))
+    return 0;
+  return st::dense_fwd_plan(dtype, batch, queries, keys, heads, head_dim).total;
+}
+
 int st_dense_fwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_t heads,
                  int64_t head_dim, int64_t block_size, const void* q, const void* k,
                  const void* v, const int64_t* positions, void* out, float* rc, float* pr,
-                 float* zr, float* z, void* stream) {
+                 float* zr, float* z, void* workspace, size_t workspace_bytes, void* stream) {
   int e;
   if ((e = check_dtype(dtype)) || (e = check_sizes(batch, queries, keys, heads, head_dim, block_size)) ||
       (e = check_envelope(head_dim, block_size)))
     return e;
   if (!q || !k || !v || !positions || !out || !rc || !pr || !zr || !z)
     return fail(ST_EINVAL, "st_dense_fwd: null pointer argument");
+  const st::DenseFwdPlan plan = st::dense_fwd_plan(dtype, batch, queries, keys, heads, head_dim);
+  if (workspace_bytes < plan.total || (plan.total && !workspace))
+    return fail(ST_EINVAL, "st_dense_fwd: workspace of %zu bytes, %zu needed", workspace_bytes, plan.total);
+  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+    return fail(ST_EINVAL, "st_dense_fwd: workspace must be 256-byte aligned");
   st::DenseArgs a = {};
   a.q = q; a.k = k; a.v = v; a.pos = positions;
   a.out = out; a.rc = rc; a.pr = pr; a.zr = zr; a.z = z;
+  if (plan.total) {
+    char* ws = reinterpret_cast<char*>(workspace);
+    a.fw0 = reinterpret_cast<float*>(ws);
+    a.fw1 = reinterpret_cast<float*>(ws + plan.off_w1);
+    a.fstat = reinterpret_cast<float*>(ws + plan.off_stat);
+    a.fflag = reinterpret_cast<int*>(ws + plan.off_flag);
+    // a row tile longer than half the longest possible one runs as two pieces
+    a.f_split = (int)((keys + 127) / 128 + 1) / 2;
+  }
   a.B = (int)batch; a.Q = (int)queries; a.N = (int)keys; a.H = (int)heads; a.D = (int)head_dim;
   a.block = (int)block_size; a.logb = log2i(block_size);
   a.scale = 1.f / sqrtf((float)head_dim);

@@ -36,6 +36,13 @@ struct DenseArgs {
   float* q_part;          // dQ partials, [item][piece][wave][register][lane]
   float* k_part;          // dK/dV partials, same order
   int q_split, k_split;   // items with more tiles than this run as two pieces
+  // pipelined forward: a row tile with more than f_split key tiles runs as
+  // two pieces whose partial results dense_fwd_merge combines (null: never)
+  float* fw0;             // [item][128 rows][D] remote mean of piece 0
+  float* fw1;             // [item][128 rows][D] local mean of piece 1
+  float* fstat;           // [item][128 rows][8] partial statistics
+  int* fflag;             // [item] 1 if the item was split
+  int f_split;
   int B, Q, N, H, D;
   int block, logb;
   int Qp, nblk;           // Q rounded up to 64; key blocks in whole 128-key tiles
@@ -46,6 +53,14 @@ struct DenseArgs {
 // Each returns hipSuccess or the launch error; the arguments were validated
 // by the caller (dtype, head_dim <= 256, block a power of two in [2,128]).
 hipError_t launch_dense_fwd(int dtype, const DenseArgs& a, hipStream_t stream);
+// Workspace of the pipelined forward (0 when the generic kernel runs): the
+// split-item partials, indexed by row tile.
+struct DenseFwdPlan {
+  bool fast;
+  int n_qtiles;
+  size_t off_w1, off_stat, off_flag, total;
+};
+DenseFwdPlan dense_fwd_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t H, int64_t D);
 // Pipelined forward for 16-bit inputs with head_dim 64 or 128.
 bool dense_fwd_fast_supported(int dtype, const DenseArgs& a);
 hipError_t launch_dense_fwd_fast(int dtype, const DenseArgs& a, hipStream_t stream);

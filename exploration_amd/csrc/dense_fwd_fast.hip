@@ -40,7 +40,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int col = lane & 31, half = lane >> 5;
   const int BH = a.B * a.H;
   const int bh = blockIdx.x % BH;
-  const int qt = n_qtiles - 1 - (int)(blockIdx.x / BH);  // longest causal rows first
+  // all first pieces (longest causal rows first), then all second pieces
+  const int kq = (int)(blockIdx.x / BH);
+  const int piece = kq >= n_qtiles;
+  const int qt = n_qtiles - 1 - (piece ? kq - n_qtiles : kq);
   const int bi = bh / a.H, hh = bh % a.H;
   const int row = qt * 32 * WAVES + wave * 32 + col;
   const bool row_in = row < a.Q;
@@ -76,11 +79,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // remote tiles ending at or below every valid row's remote limit need no
   // masks (padding rows are zeroed when the row is finalised)
   const int full_remote = rg3 == 0x7fffffff ? 0 : rg3 / NT;
-  const int n_remote = (rg0 + NT - 1) / NT;
+  const int n_remote_all = (rg0 + NT - 1) / NT;
   const int lt0 = rg2 >= 0 ? rg1 / NT : 0;
   const int n_local = rg2 >= 0 ? rg2 / NT - lt0 + 1 : 0;
-  const int total = n_remote + n_local;
-  auto tile_of = [&](int i) { return i < n_remote ? i : lt0 + (i - n_remote); };
+  // A long row tile runs as two pieces (causal load balance): piece 0 takes
+  // remote tiles [0, h), piece 1 remote tiles [h, n_remote_all) and the local
+  // tiles; dense_fwd_merge combines their partial results.
+  const bool split = a.fw0 != nullptr && n_remote_all + n_local > a.f_split;
+  if (piece && !split) return;  // whole workgroup
+  const int item = bh * n_qtiles + qt;
+  const int hsplit = split ? min((n_remote_all + n_local + 1) / 2, n_remote_all) : n_remote_all;
+  const int rs = piece ? hsplit : 0;                              // first remote tile of this piece
+  const int n_remote = piece ? n_remote_all - hsplit : hsplit;    // remote tiles of this piece
+  const bool with_local = !split || piece;
+  const int total = n_remote + (with_local ? n_local : 0);
+  auto tile_of = [&](int i) { return i < n_remote ? rs + i : lt0 + (i - n_remote); };
 
   const T* kg = reinterpret_cast<const T*>(a.k) + ((int64_t)bi * N * H + hh) * D;
   const T* vg = reinterpret_cast<const T*>(a.v) + ((int64_t)bi * N * H + hh) * D;
@@ -138,13 +151,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // End of the remote pass: its statistics, and its mean parked in rc (one
   // burst of stores that drains while the local tiles run; registers cannot
   // hold two accumulators next to the pipelined loop).
+  const bool park_rc = !(split && piece == 0);  // piece 0 writes its mean in the epilogue
   auto finish_remote = [&]() {
     zs_r += swap_halves(zs_r);
     dr += swap_halves(dr);
     log_zr = log_mass(m_r, zs_r);
     lr = dr > 0.f ? log_mass(m_r, dr) - fast_log2(zs_r) * kLn2 : kNegInf;
     const float inv = dr > 0.f ? 1.f / dr : 0.f;
-    if (row_in) {
+    if (row_in && park_rc) {
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -155,8 +169,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
           *reinterpret_cast<f32x4*>(a.rc + obase + d) = val;
         }
     }
+    // the local pass starts from zero; piece 0 keeps its remote sums for
+    // the epilogue
+    if (park_rc) {
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) acc[dt] = zero16();
+      for (int dt = 0; dt < NDT; ++dt) acc[dt] = zero16();
+    }
   };
 
   // Software pipeline over the tile sequence. Iteration i issues, in one
@@ -349,7 +367,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
   // unmasked remote tiles in pairs (an even count; an odd last one joins the
   // masked loop), then every remaining tile through the masked variant
-  const int n_fast = (full_remote < n_remote ? full_remote : n_remote) & ~1;
+  const int n_fast = max(0, min(full_remote, rs + n_remote) - rs) & ~1;
   int i = 0;
   for (; i < n_fast; i += 2) {
     iteration.template operator()<0, false>(i);
@@ -372,6 +390,50 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // local statistics (zs now holds the local denominator); padding rows,
   // which skipped masks on full remote tiles, have no mass at all
   const float zsum = zs_l + swap_halves(zs_l);
+  constexpr int RLD = DP + 4;  // fp32 staging stride: conflict-free 16-byte writes
+  static_assert(32 * RLD * 4 + 32 * 4 <= TILE * (int)sizeof(T), "staging fits one buffer");
+  float* lst = reinterpret_cast<float*>(wave == 0 ? k0s : (wave == 1 ? k1s : (wave == 2 ? v0s : v1s)));
+  // acc * f (per row) into this wave's staging buffer, rows [32 wave, +32)
+  auto stage_acc = [&](float f) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = 32 * dt + 8 * i + 4 * half;
+        const f32x4 lv = {acc[dt][4 * i] * f, acc[dt][4 * i + 1] * f, acc[dt][4 * i + 2] * f,
+                          acc[dt][4 * i + 3] * f};
+        *reinterpret_cast<f32x4*>(lst + col * RLD + d) = lv;
+      }
+  };
+  if (a.fw0 != nullptr && piece == 0 && threadIdx.x == 0) a.fflag[item] = split ? 1 : 0;
+  if (split) {
+    // partial results of this piece: statistics per row, and the remote mean
+    // (piece 0) or the local mean (piece 1) as rows, for dense_fwd_merge
+    const int lrow = wave * 32 + col;
+    float* st8 = a.fstat + ((size_t)item * 128 + lrow) * 8;
+    if (half == 0 && row_in) {
+      if (piece == 0) {
+        st8[0] = m_r; st8[1] = zs_r; st8[2] = dr;
+      } else {
+        st8[3] = m_r; st8[4] = zs_r; st8[5] = dr; st8[6] = m_l; st8[7] = zsum;
+      }
+    }
+    const float f = piece == 0 ? (dr > 0.f ? 1.f / dr : 0.f) : (zsum > 0.f ? 1.f / zsum : 0.f);
+    float* dst = (piece == 0 ? a.fw0 : a.fw1) + (size_t)item * 128 * D;
+    __syncthreads();  // every wave is done with the K/V buffers
+    stage_acc(f);
+    __syncthreads();
+    constexpr int RL = DP / 4;  // lanes per row, 4 floats each
+    const int row0 = qt * 32 * WAVES + wave * 32;
+#pragma unroll
+    for (int it = 0; it < 32 * RL / 64; ++it) {
+      const int r = (it * 64 + lane) / RL, c = ((it * 64 + lane) % RL) * 4;
+      if (row0 + r < a.Q)
+        *reinterpret_cast<f32x4*>(dst + (int64_t)(wave * 32 + r) * D + c) =
+            *reinterpret_cast<const f32x4*>(lst + r * RLD + c);
+    }
+    return;
+  }
   const float dl = p >= 0 ? zsum : 0.f;
   const float ll = p >= 0 ? log_mass(m_l, dl) : kNegInf;
   if (p < 0) {
@@ -394,20 +456,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // in one 32 KiB K/V buffer (free after the drain) and then reads, combines
   // and writes whole rows. With lane = row, direct global accesses would
   // touch 64 cache lines per instruction.
-  constexpr int RLD = DP + 4;  // fp32 staging stride: conflict-free 16-byte writes
-  static_assert(32 * RLD * 4 + 32 * 4 <= TILE * (int)sizeof(T), "staging fits one buffer");
   __syncthreads();  // every wave is done with the K/V buffers
-  float* lst = reinterpret_cast<float*>(wave == 0 ? k0s : (wave == 1 ? k1s : (wave == 2 ? v0s : v1s)));
   float* wst = lst + 32 * RLD;  // per-row prem
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d = 32 * dt + 8 * i + 4 * half;
-      const f32x4 lv = {acc[dt][4 * i] * linv, acc[dt][4 * i + 1] * linv, acc[dt][4 * i + 2] * linv,
-                        acc[dt][4 * i + 3] * linv};
-      *reinterpret_cast<f32x4*>(lst + col * RLD + d) = lv;
-    }
+  stage_acc(linv);
   if (half == 0) wst[col] = prem;
   // the parked rc stores of this wave are visible to all its lanes
   __threadfence_block();
@@ -447,10 +498,76 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
 }
 
+// Combination of the two pieces of every split row tile: remote partials
+// (max m, row sum zs, sum of squared block sums dr, all at scale 2^-m, and
+// the remote means) merged at the common max, then the gate with the local
+// partial of piece 1 as in the single-piece epilogue. Threads run along the
+// head dimension (DP/4 per row, 4 values each): every access is
+// row-contiguous.
+template <typename T, int DP>
+__global__ __launch_bounds__(256) void dense_fwd_merge_kernel(DenseArgs a, int n_qtiles) {
+  const int item = blockIdx.x;
+  if (a.fflag[item] == 0) return;
+  const int bh = item / n_qtiles, qt = item % n_qtiles;
+  const int bi = bh / a.H, hh = bh % a.H;
+  const int64_t H = a.H, D = a.D;
+  constexpr int RL = DP / 4;     // threads per row
+  constexpr int RPP = 256 / RL;  // rows per pass
+  const int r_in = threadIdx.x / RL, c = (threadIdx.x % RL) * 4;
+  typedef T T4 __attribute__((ext_vector_type(4)));
+  for (int r0 = 0; r0 < 128; r0 += RPP) {
+    const int lrow = r0 + r_in, row = qt * 128 + lrow;
+    if (row >= a.Q) break;
+    const float* st8 = a.fstat + ((size_t)item * 128 + lrow) * 8;
+    const float m0 = st8[0], zs0 = st8[1], dr0 = st8[2];
+    const float m1 = st8[3], zs1 = st8[4], dr1 = st8[5], ml = st8[6], zl = st8[7];
+    const int64_t p = a.pos[(int64_t)bi * a.Q + row];
+    const float mx = fmaxf(m0, m1);
+    float zs = 0.f, w0 = 0.f, w1 = 0.f;
+    if (mx != kNegInf) {
+      const float e0 = fast_exp2(m0 - mx), e1 = fast_exp2(m1 - mx);
+      zs = zs0 * e0 + zs1 * e1;
+      w0 = dr0 * e0 * e0;
+      w1 = dr1 * e1 * e1;
+    }
+    const float drs = w0 + w1;
+    float log_zr = zs > 0.f ? log_mass(mx, zs) : kNegInf;
+    float lr = drs > 0.f ? log_mass(mx, drs) - fast_log2(zs) * kLn2 : kNegInf;
+    float ll = zl > 0.f ? log_mass(ml, zl) : kNegInf;
+    if (p < 0) { lr = kNegInf; ll = kNegInf; log_zr = kNegInf; }
+    const float tot = logaddexp(lr, ll);
+    const float safe_total = tot == kNegInf ? 0.f : tot;
+    const float prem = lr == kNegInf ? 0.f : __expf(lr - safe_total);
+    const float ploc = ll == kNegInf ? 0.f : __expf(ll - safe_total);
+    const float a0 = drs > 0.f ? prem * (w0 / drs) : 0.f, a1 = drs > 0.f ? prem * (w1 / drs) : 0.f;
+    const int64_t g = (((int64_t)bi * a.Q + row) * H + hh) * D + c;
+    const size_t w = ((size_t)item * 128 + lrow) * D + c;
+    const f32x4 mean0 = *reinterpret_cast<const f32x4*>(a.fw0 + w);
+    const f32x4 mean1 = *reinterpret_cast<const f32x4*>(a.rc + g);
+    const f32x4 meanl = *reinterpret_cast<const f32x4*>(a.fw1 + w);
+    f32x4 rc;
+    T4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      rc[j] = a0 * mean0[j] + a1 * mean1[j];
+      o[j] = from_float<T>(rc[j] + ploc * meanl[j]);
+    }
+    *reinterpret_cast<f32x4*>(a.rc + g) = rc;
+    *reinterpret_cast<T4*>(reinterpret_cast<T*>(a.out) + g) = o;
+    if (c == 0) {
+      const int64_t sidx = ((int64_t)bi * a.Q + row) * H + hh;
+      a.pr[sidx] = prem;
+      a.zr[sidx] = log_zr;
+      a.z[sidx] = tot;
+    }
+  }
+}
+
 template <typename T, int DP>
 static hipError_t launch_fast(const DenseArgs& a, hipStream_t stream) {
   const int n_qtiles = (a.Q + 127) / 128;
-  dim3 grid((unsigned)(n_qtiles * a.B * a.H));
+  const unsigned items = (unsigned)(n_qtiles * a.B * a.H);
+  dim3 grid(a.fw0 != nullptr ? 2 * items : items);
   auto go = [&]<int LOGB>() {
     hipLaunchKernelGGL((dense_fwd_fast_kernel<T, DP, LOGB>), grid, dim3(256), 0, stream, a, n_qtiles);
   };
@@ -463,7 +580,30 @@ static hipError_t launch_fast(const DenseArgs& a, hipStream_t stream) {
     case 6: go.template operator()<6>(); break;
     default: go.template operator()<7>(); break;
   }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.fw0 == nullptr) return e;
+  hipLaunchKernelGGL((dense_fwd_merge_kernel<T, DP>), dim3(items), dim3(256), 0, stream, a, n_qtiles);
   return hipGetLastError();
+}
+
+namespace {
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+}  // namespace
+
+DenseFwdPlan dense_fwd_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t H, int64_t D) {
+  DenseFwdPlan p = {};
+  p.fast = (dtype == kBF16 || dtype == kF16) && (D == 64 || D == 128);
+  if (!p.fast) return p;
+  p.n_qtiles = (int)((Q + 127) / 128);
+  const int64_t n_ktiles = (N + 127) / 128;
+  if (n_ktiles < 4) return p;  // no row tile long enough to split: no workspace
+  const size_t items = (size_t)(B * H) * p.n_qtiles;
+  const size_t w = align256(items * 128 * (size_t)D * sizeof(float));
+  p.off_w1 = w;
+  p.off_stat = 2 * w;
+  p.off_flag = p.off_stat + align256(items * 128 * 8 * sizeof(float));
+  p.total = p.off_flag + align256(items * sizeof(int));
+  return p;
 }
 
 bool dense_fwd_fast_supported(int dtype, const DenseArgs& a) {

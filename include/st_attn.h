@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ST_ABI_VERSION 2
+#define ST_ABI_VERSION 3
 
 #define ST_DTYPE_F32 0
 #define ST_DTYPE_F16 1
@@ -56,13 +56,25 @@ const char* st_last_error(void);
  * [2, 128], head_dim <= 256 (here also a multiple of 8). */
 int st_dense_supported(int dtype, int64_t head_dim, int64_t block_size);
 
+/* Bytes of device workspace st_dense_fwd needs for this problem (0 if none
+ * or if the arguments are invalid). The pipelined 16-bit path (head_dim 64
+ * or 128) runs the longest causal row tiles as two pieces and merges their
+ * partial results: per 128-row tile 2 x 128 x head_dim floats of partial
+ * means, 128 x 8 floats of statistics and a flag. No reference counterpart:
+ * the reference's Triton forward allocates its own buffers
+ * (st/ops/kernels/dense.py:200-203). */
+size_t st_dense_fwd_workspace_bytes(int dtype, int64_t batch, int64_t queries, int64_t keys,
+                                    int64_t heads, int64_t head_dim, int64_t block_size);
+
 /* Gated dense forward. Replaces the `_forward` launch of
  * st/ops/kernels/dense.py:197-217 (kernel st/ops/kernels/dense.py:32-86).
- * Writes out (dtype) and the saved statistics rc, pr, zr, z (float). */
+ * Writes out (dtype) and the saved statistics rc, pr, zr, z (float).
+ * workspace: st_dense_fwd_workspace_bytes() bytes, 256-byte aligned (may be
+ * NULL when that is 0). */
 int st_dense_fwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_t heads,
                  int64_t head_dim, int64_t block_size, const void* q, const void* k,
                  const void* v, const int64_t* positions, void* out, float* rc, float* pr,
-                 float* zr, float* z, void* stream);
+                 float* zr, float* z, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Bytes of device workspace st_dense_bwd needs for this problem (0 if the
  * arguments are invalid): per-row delta and rho, plus, on the pipelined

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in declared_functions():
         assert hasattr(lib, name), f"{name} missing from libst_attn.so"
-    assert lib.st_abi_version() == 2
+    assert lib.st_abi_version() == 3
     assert lib.st_last_error() == b""
 
 
@@ -50,16 +50,16 @@ def test_argument_errors_map_to_value_error():
     """Argument checks run on the host and fail before any HIP call."""
     lib = _lib.load()
     null = None
-    status = lib.st_dense_fwd(2, 1, 1, 1, 1, 64, 16, *([null] * 3), null, null, *([null] * 4), null)
+    status = lib.st_dense_fwd(2, 1, 1, 1, 1, 64, 16, *([null] * 3), null, null, *([null] * 4), null, 0, null)
     assert status == _lib.ST_EINVAL
     assert b"null pointer" in lib.st_last_error()
     with pytest.raises(ValueError, match="null pointer"):
         _lib.check(status, lib)
-    status = lib.st_dense_fwd(2, 1, 1, 1, 1, 64, 3, *([null] * 3), null, null, *([null] * 4), null)
+    status = lib.st_dense_fwd(2, 1, 1, 1, 1, 64, 3, *([null] * 3), null, null, *([null] * 4), null, 0, null)
     assert status == _lib.ST_EUNSUPPORTED
     with pytest.raises(ValueError, match="power of two"):
         _lib.check(status, lib)
-    status = lib.st_dense_fwd(2, 0, 1, 1, 1, 64, 16, *([null] * 3), null, null, *([null] * 4), null)
+    status = lib.st_dense_fwd(2, 0, 1, 1, 1, 64, 16, *([null] * 3), null, null, *([null] * 4), null, 0, null)
     assert status == _lib.ST_EINVAL
     status = lib.st_sparse_select(4, 10, 0, 0, null, null, null, null, null)
     assert status == _lib.ST_EINVAL
