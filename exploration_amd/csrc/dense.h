@@ -36,13 +36,16 @@ struct DenseArgs {
   float* q_part;          // dQ partials, [item][piece][wave][register][lane]
   float* k_part;          // dK/dV partials, same order
   int q_split, k_split;   // items with more tiles than this run as two pieces
-  // pipelined forward: a row tile with more than f_split key tiles runs as
-  // two pieces whose partial results dense_fwd_merge combines (null: never)
+  // pipelined forward: a long row tile runs as two pieces whose partial
+  // results dense_fwd_merge combines (fw0 null: never). Slot mode splits a
+  // tile with more than f_split key tiles in halves; pair mode (f_pair) runs
+  // row tiles n-1-j and j as one pair of workgroups with equal tile counts.
   float* fw0;             // [item][128 rows][D] remote mean of piece 0
   float* fw1;             // [item][128 rows][D] local mean of piece 1
   float* fstat;           // [item][128 rows][8] partial statistics
   int* fflag;             // [item] 1 if the item was split
   int f_split;
+  int f_pair;
   int B, Q, N, H, D;
   int block, logb;
   int Qp, nblk;           // Q rounded up to 64; key blocks in whole 128-key tiles

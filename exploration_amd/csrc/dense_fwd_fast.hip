@@ -34,61 +34,127 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   __shared__ __attribute__((aligned(16))) T k1s[TILE];
   __shared__ __attribute__((aligned(16))) T v0s[TILE];
   __shared__ __attribute__((aligned(16))) T v1s[TILE];
-  __shared__ int range[4][WAVES];
+  __shared__ int range[2][4][WAVES];  // two tiles: this one and the pair partner
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 31, half = lane >> 5;
   const int BH = a.B * a.H;
-  const int bh = blockIdx.x % BH;
-  // all first pieces (longest causal rows first), then all second pieces
-  const int kq = (int)(blockIdx.x / BH);
-  const int piece = kq >= n_qtiles;
-  const int qt = n_qtiles - 1 - (piece ? kq - n_qtiles : kq);
+  const int bh = blockIdx.x % BH, slot = blockIdx.x / BH;
   const int bi = bh / a.H, hh = bh % a.H;
-  const int row = qt * 32 * WAVES + wave * 32 + col;
-  const bool row_in = row < a.Q;
   const int64_t H = a.H, D = a.D, N = a.N;
-  const int64_t p = row_in ? a.pos[(int64_t)bi * a.Q + row] : -1;
   constexpr int b = 1 << LOGB;
 
-  int rlim = 0, llo = 0, lhi = -1;
-  if (p >= 0) {
-    const int64_t c = p >> LOGB;
-    const int64_t lo = (c - 1) * b > 0 ? (c - 1) * b : 0;
-    rlim = (int)(lo < N ? lo : N);
-    llo = (int)lo;
-    lhi = (int)(p < N - 1 ? p : N - 1);
+  // The job of this workgroup: row tile qt, kind 0 (the tile whole or its
+  // first piece), 1 (its second piece; nothing if unsplit) or 2 (whole).
+  // Slot mode: 2 n_qtiles slots per head, slot k < n_qtiles takes kind 0 of
+  // row tile n_qtiles-1-k, slot n_qtiles+k kind 1 of it (longest causal rows
+  // first). Pair mode: row tiles L = n-1-j and S = j form pair j; slot j
+  // (j < n/2) takes kind 0 of L, slot n/2+j kind 1 of L, then an odd middle
+  // tile, then the S tiles whole, longest first. L is cut so that, under
+  // causal positions, its second piece plus S matches its first piece: the
+  // dispatcher hands each S tile to the compute unit that finishes first,
+  // which is the one that ran the short second piece of the same pair.
+  int qt, kind, partner = -1;
+  if (a.f_pair) {
+    const int P = n_qtiles / 2, odd = n_qtiles & 1;
+    if (slot < 2 * P) {
+      const int j = slot < P ? slot : slot - P;
+      qt = n_qtiles - 1 - j;
+      kind = slot >= P;
+      partner = j;
+    } else if (slot < 2 * P + odd) {
+      qt = P;
+      kind = 2;
+    } else {
+      qt = 3 * P + odd - 1 - slot;
+      kind = 2;
+    }
+  } else {
+    kind = slot >= n_qtiles;
+    qt = n_qtiles - 1 - (kind ? slot - n_qtiles : slot);
   }
-  // workgroup ranges: max remote limit, min / max local key, min remote
-  // limit of the rows with a local window
-  {
-    const bool win = lhi >= llo;
-    const int r0 = wave_max(rlim), r1 = wave_min(win ? llo : 0x7fffffff);
-    const int r2 = wave_max(win ? lhi : -1), r3 = wave_min(win ? rlim : 0x7fffffff);
-    if (lane == 0) { range[0][wave] = r0; range[1][wave] = r1; range[2][wave] = r2; range[3][wave] = r3; }
-  }
-  __syncthreads();
-  int rg0 = range[0][0], rg1 = range[1][0], rg2 = range[2][0], rg3 = range[3][0];
+
+  // Per lane: the row's remote limit and local window [llo, lhi] for row
+  // tile qt.
+  struct RowKeys {
+    int64_t p;
+    int rlim, llo, lhi;
+  };
+  auto row_keys = [&](int qt) -> RowKeys {
+    const int row = qt * 32 * WAVES + wave * 32 + col;
+    RowKeys r = {row < a.Q ? a.pos[(int64_t)bi * a.Q + row] : -1, 0, 0, -1};
+    if (r.p >= 0) {
+      const int64_t c = r.p >> LOGB;
+      const int64_t lo = (c - 1) * b > 0 ? (c - 1) * b : 0;
+      r.rlim = (int)(lo < N ? lo : N);
+      r.llo = (int)lo;
+      r.lhi = (int)(r.p < N - 1 ? r.p : N - 1);
+    }
+    return r;
+  };
+  // Workgroup key ranges of a row tile (slot k of the LDS table; one barrier):
+  // max remote limit, min / max local key, min remote limit of the rows with
+  // a local window; and from them the tile counts.
+  struct TileKeys {
+    int n_remote_all, lt0, n_local, full_remote;
+  };
+  auto tile_keys = [&](const RowKeys& r, int k) -> TileKeys {
+    const bool win = r.lhi >= r.llo;
+    const int r0 = wave_max(r.rlim), r1 = wave_min(win ? r.llo : 0x7fffffff);
+    const int r2 = wave_max(win ? r.lhi : -1), r3 = wave_min(win ? r.rlim : 0x7fffffff);
+    if (lane == 0) {
+      range[k][0][wave] = r0;
+      range[k][1][wave] = r1;
+      range[k][2][wave] = r2;
+      range[k][3][wave] = r3;
+    }
+    __syncthreads();
+    int rg0 = range[k][0][0], rg1 = range[k][1][0], rg2 = range[k][2][0], rg3 = range[k][3][0];
 #pragma unroll
-  for (int w = 1; w < WAVES; ++w) {
-    rg0 = max(rg0, range[0][w]);
-    rg1 = min(rg1, range[1][w]);
-    rg2 = max(rg2, range[2][w]);
-    rg3 = min(rg3, range[3][w]);
+    for (int w = 1; w < WAVES; ++w) {
+      rg0 = max(rg0, range[k][0][w]);
+      rg1 = min(rg1, range[k][1][w]);
+      rg2 = max(rg2, range[k][2][w]);
+      rg3 = min(rg3, range[k][3][w]);
+    }
+    TileKeys t;
+    // remote tiles ending at or below every valid row's remote limit need
+    // no masks (padding rows are zeroed when the row is finalised)
+    t.full_remote = rg3 == 0x7fffffff ? 0 : rg3 / NT;
+    t.n_remote_all = (rg0 + NT - 1) / NT;
+    t.lt0 = rg2 >= 0 ? rg1 / NT : 0;
+    t.n_local = rg2 >= 0 ? rg2 / NT - t.lt0 + 1 : 0;
+    return t;
+  };
+
+  const int row = qt * 32 * WAVES + wave * 32 + col;
+  const bool row_in = row < a.Q;
+  const RowKeys rk = row_keys(qt);
+  const int64_t p = rk.p;
+  const int rlim = rk.rlim, llo = rk.llo, lhi = rk.lhi;
+  const TileKeys tk = tile_keys(rk, 0);
+  const int full_remote = tk.full_remote, n_remote_all = tk.n_remote_all, lt0 = tk.lt0, n_local = tk.n_local;
+  const int n_all = n_remote_all + n_local;
+  // A split row tile runs as two pieces: piece 0 takes remote tiles [0, h),
+  // piece 1 remote tiles [h, n_remote_all) and the local tiles;
+  // dense_fwd_merge combines their partial results.
+  bool split = false;
+  int hsplit = n_remote_all;
+  if (a.fw0 != nullptr && kind != 2) {
+    if (a.f_pair) {
+      // equal shares of the pair's key tiles (identical in both workgroups)
+      const TileKeys to = tile_keys(row_keys(partner), 1);
+      hsplit = min(n_remote_all, (n_all + to.n_remote_all + to.n_local + 1) / 2);
+      split = hsplit > 0 && hsplit < n_all;
+    } else if (n_all > a.f_split) {
+      split = true;
+      hsplit = min((n_all + 1) / 2, n_remote_all);
+    }
+    if (!split) hsplit = n_remote_all;
   }
-  // remote tiles ending at or below every valid row's remote limit need no
-  // masks (padding rows are zeroed when the row is finalised)
-  const int full_remote = rg3 == 0x7fffffff ? 0 : rg3 / NT;
-  const int n_remote_all = (rg0 + NT - 1) / NT;
-  const int lt0 = rg2 >= 0 ? rg1 / NT : 0;
-  const int n_local = rg2 >= 0 ? rg2 / NT - lt0 + 1 : 0;
-  // A long row tile runs as two pieces (causal load balance): piece 0 takes
-  // remote tiles [0, h), piece 1 remote tiles [h, n_remote_all) and the local
-  // tiles; dense_fwd_merge combines their partial results.
-  const bool split = a.fw0 != nullptr && n_remote_all + n_local > a.f_split;
+  const int piece = kind == 1;
   if (piece && !split) return;  // whole workgroup
   const int item = bh * n_qtiles + qt;
-  const int hsplit = split ? min((n_remote_all + n_local + 1) / 2, n_remote_all) : n_remote_all;
   const int rs = piece ? hsplit : 0;                              // first remote tile of this piece
   const int n_remote = piece ? n_remote_all - hsplit : hsplit;    // remote tiles of this piece
   const bool with_local = !split || piece;
@@ -405,7 +471,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         *reinterpret_cast<f32x4*>(lst + col * RLD + d) = lv;
       }
   };
-  if (a.fw0 != nullptr && piece == 0 && threadIdx.x == 0) a.fflag[item] = split ? 1 : 0;
+  if (a.fw0 != nullptr && !piece && threadIdx.x == 0) a.fflag[item] = split ? 1 : 0;
   if (split) {
     // partial results of this piece: statistics per row, and the remote mean
     // (piece 0) or the local mean (piece 1) as rows, for dense_fwd_merge
@@ -501,73 +567,97 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 // Combination of the two pieces of every split row tile: remote partials
 // (max m, row sum zs, sum of squared block sums dr, all at scale 2^-m, and
 // the remote means) merged at the common max, then the gate with the local
-// partial of piece 1 as in the single-piece epilogue. Threads run along the
-// head dimension (DP/4 per row, 4 values each): every access is
-// row-contiguous.
+// partial of piece 1 as in the single-piece epilogue. DP/8 threads per row,
+// 8 values each: every access is row-contiguous, and all loads of a thread
+// are issued before its arithmetic.
 template <typename T, int DP>
 __global__ __launch_bounds__(256) void dense_fwd_merge_kernel(DenseArgs a, int n_qtiles) {
-  const int item = blockIdx.x;
+  constexpr int TR = DP / 8;      // threads per row
+  constexpr int RPW = 256 / TR;   // rows per workgroup
+  constexpr int WPI = 128 / RPW;  // workgroups per row tile
+  const int item = blockIdx.x / WPI;
   if (a.fflag[item] == 0) return;
   const int bh = item / n_qtiles, qt = item % n_qtiles;
   const int bi = bh / a.H, hh = bh % a.H;
+  const int lrow = (blockIdx.x % WPI) * RPW + threadIdx.x / TR, row = qt * 128 + lrow;
+  if (row >= a.Q) return;
+  const int c = (threadIdx.x % TR) * 8;
   const int64_t H = a.H, D = a.D;
-  constexpr int RL = DP / 4;     // threads per row
-  constexpr int RPP = 256 / RL;  // rows per pass
-  const int r_in = threadIdx.x / RL, c = (threadIdx.x % RL) * 4;
-  typedef T T4 __attribute__((ext_vector_type(4)));
-  for (int r0 = 0; r0 < 128; r0 += RPP) {
-    const int lrow = r0 + r_in, row = qt * 128 + lrow;
-    if (row >= a.Q) break;
-    const float* st8 = a.fstat + ((size_t)item * 128 + lrow) * 8;
-    const float m0 = st8[0], zs0 = st8[1], dr0 = st8[2];
-    const float m1 = st8[3], zs1 = st8[4], dr1 = st8[5], ml = st8[6], zl = st8[7];
-    const int64_t p = a.pos[(int64_t)bi * a.Q + row];
-    const float mx = fmaxf(m0, m1);
-    float zs = 0.f, w0 = 0.f, w1 = 0.f;
-    if (mx != kNegInf) {
-      const float e0 = fast_exp2(m0 - mx), e1 = fast_exp2(m1 - mx);
-      zs = zs0 * e0 + zs1 * e1;
-      w0 = dr0 * e0 * e0;
-      w1 = dr1 * e1 * e1;
-    }
-    const float drs = w0 + w1;
-    float log_zr = zs > 0.f ? log_mass(mx, zs) : kNegInf;
-    float lr = drs > 0.f ? log_mass(mx, drs) - fast_log2(zs) * kLn2 : kNegInf;
-    float ll = zl > 0.f ? log_mass(ml, zl) : kNegInf;
-    if (p < 0) { lr = kNegInf; ll = kNegInf; log_zr = kNegInf; }
-    const float tot = logaddexp(lr, ll);
-    const float safe_total = tot == kNegInf ? 0.f : tot;
-    const float prem = lr == kNegInf ? 0.f : __expf(lr - safe_total);
-    const float ploc = ll == kNegInf ? 0.f : __expf(ll - safe_total);
-    const float a0 = drs > 0.f ? prem * (w0 / drs) : 0.f, a1 = drs > 0.f ? prem * (w1 / drs) : 0.f;
-    const int64_t g = (((int64_t)bi * a.Q + row) * H + hh) * D + c;
-    const size_t w = ((size_t)item * 128 + lrow) * D + c;
-    const f32x4 mean0 = *reinterpret_cast<const f32x4*>(a.fw0 + w);
-    const f32x4 mean1 = *reinterpret_cast<const f32x4*>(a.rc + g);
-    const f32x4 meanl = *reinterpret_cast<const f32x4*>(a.fw1 + w);
+  const int64_t g = (((int64_t)bi * a.Q + row) * H + hh) * D + c;
+  const size_t w = ((size_t)item * 128 + lrow) * D + c;
+  const float* st8 = a.fstat + ((size_t)item * 128 + lrow) * 8;
+  const f32x4 sa = *reinterpret_cast<const f32x4*>(st8), sb = *reinterpret_cast<const f32x4*>(st8 + 4);
+  const int64_t p = a.pos[(int64_t)bi * a.Q + row];
+  f32x4 mean0[2], mean1[2], meanl[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    mean0[h] = *reinterpret_cast<const f32x4*>(a.fw0 + w + 4 * h);
+    mean1[h] = *reinterpret_cast<const f32x4*>(a.rc + g + 4 * h);
+    meanl[h] = *reinterpret_cast<const f32x4*>(a.fw1 + w + 4 * h);
+  }
+  const float m0 = sa[0], zs0 = sa[1], dr0 = sa[2];
+  const float m1 = sa[3], zs1 = sb[0], dr1 = sb[1], ml = sb[2], zl = sb[3];
+  const float mx = fmaxf(m0, m1);
+  float zs = 0.f, w0 = 0.f, w1 = 0.f;
+  if (mx != kNegInf) {
+    const float e0 = fast_exp2(m0 - mx), e1 = fast_exp2(m1 - mx);
+    zs = zs0 * e0 + zs1 * e1;
+    w0 = dr0 * e0 * e0;
+    w1 = dr1 * e1 * e1;
+  }
+  const float drs = w0 + w1;
+  float log_zr = zs > 0.f ? log_mass(mx, zs) : kNegInf;
+  float lr = drs > 0.f ? log_mass(mx, drs) - fast_log2(zs) * kLn2 : kNegInf;
+  float ll = zl > 0.f ? log_mass(ml, zl) : kNegInf;
+  if (p < 0) { lr = kNegInf; ll = kNegInf; log_zr = kNegInf; }
+  const float tot = logaddexp(lr, ll);
+  const float safe_total = tot == kNegInf ? 0.f : tot;
+  const float prem = lr == kNegInf ? 0.f : __expf(lr - safe_total);
+  const float ploc = ll == kNegInf ? 0.f : __expf(ll - safe_total);
+  const float a0 = drs > 0.f ? prem * (w0 / drs) : 0.f, a1 = drs > 0.f ? prem * (w1 / drs) : 0.f;
+  typedef T T8 __attribute__((ext_vector_type(8)));
+  T8 o;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
     f32x4 rc;
-    T4 o;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      rc[j] = a0 * mean0[j] + a1 * mean1[j];
-      o[j] = from_float<T>(rc[j] + ploc * meanl[j]);
+      rc[j] = a0 * mean0[h][j] + a1 * mean1[h][j];
+      o[4 * h + j] = from_float<T>(rc[j] + ploc * meanl[h][j]);
     }
-    *reinterpret_cast<f32x4*>(a.rc + g) = rc;
-    *reinterpret_cast<T4*>(reinterpret_cast<T*>(a.out) + g) = o;
-    if (c == 0) {
-      const int64_t sidx = ((int64_t)bi * a.Q + row) * H + hh;
-      a.pr[sidx] = prem;
-      a.zr[sidx] = log_zr;
-      a.z[sidx] = tot;
-    }
+    *reinterpret_cast<f32x4*>(a.rc + g + 4 * h) = rc;
+  }
+  *reinterpret_cast<T8*>(reinterpret_cast<T*>(a.out) + g) = o;
+  if (c == 0) {
+    const int64_t sidx = ((int64_t)bi * a.Q + row) * H + hh;
+    a.pr[sidx] = prem;
+    a.zr[sidx] = log_zr;
+    a.z[sidx] = tot;
   }
 }
 
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
 template <typename T, int DP>
-static hipError_t launch_fast(const DenseArgs& a, hipStream_t stream) {
+static hipError_t launch_fast(const DenseArgs& args, hipStream_t stream) {
+  DenseArgs a = args;
   const int n_qtiles = (a.Q + 127) / 128;
   const unsigned items = (unsigned)(n_qtiles * a.B * a.H);
-  dim3 grid(a.fw0 != nullptr ? 2 * items : items);
+  // pair mode once slot mode's slots outnumber the compute units
+  a.f_pair = a.fw0 != nullptr && 2 * (int64_t)items > device_cus();
+  const int per_head = a.f_pair ? 3 * (n_qtiles / 2) + (n_qtiles & 1) : a.fw0 != nullptr ? 2 * n_qtiles : n_qtiles;
+  dim3 grid((unsigned)(per_head * a.B * a.H));
   auto go = [&]<int LOGB>() {
     hipLaunchKernelGGL((dense_fwd_fast_kernel<T, DP, LOGB>), grid, dim3(256), 0, stream, a, n_qtiles);
   };
@@ -582,7 +672,8 @@ static hipError_t launch_fast(const DenseArgs& a, hipStream_t stream) {
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.fw0 == nullptr) return e;
-  hipLaunchKernelGGL((dense_fwd_merge_kernel<T, DP>), dim3(items), dim3(256), 0, stream, a, n_qtiles);
+  constexpr int WPI = 128 / (256 / (DP / 8));
+  hipLaunchKernelGGL((dense_fwd_merge_kernel<T, DP>), dim3(items * WPI), dim3(256), 0, stream, a, n_qtiles);
   return hipGetLastError();
 }
 
