@@ -465,13 +465,8 @@ static hipError_t launch_bwd_t(const DenseArgs& a, hipStream_t stream) {
 
 hipError_t launch_dense_bwd(int dtype, const DenseArgs& a, hipStream_t stream) {
   if (a.tab) {
-    // pipelined path (16-bit, head_dim 64/128; the workspace carries its table)
-    const int64_t rows = (int64_t)a.B * a.Q * a.H;
-    const dim3 grid((unsigned)((rows + 3) / 4));
-    if (dtype == kBF16) hipLaunchKernelGGL((dense_bwd_pre_kernel<bf16>), grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((dense_bwd_pre_kernel<f16>), grid, dim3(256), 0, stream, a);
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    // pipelined path (16-bit, head_dim 64/128; the workspace carries its
+    // table; delta and rho come from its preparation kernel)
     return launch_dense_bwd_fast(dtype, a, stream);
   }
   switch (dtype) {

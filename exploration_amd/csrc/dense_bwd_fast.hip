@@ -18,8 +18,9 @@
 //   beyond the row's window: beta_j = +inf (P = 0), eps_j = 0.
 //
 // Kernels:
-//  * dense_bwd_rows: per row the last visible key, per 64-row tile its
-//    min/max (which row tiles a key tile must visit, and which need masks);
+//  * dense_bwd_prep: delta and rho per row; per row the last visible key,
+//    per 64-row tile its min/max (which row tiles a key tile must visit,
+//    and which need masks);
 //  * dense_bwd_dq_fast: lane = query row, the layout in which block sums are
 //    in-lane; recomputes S and dP, writes dQ and the (beta, eps) table;
 //  * dense_bwd_dkv_fast: lane = key; per element one exp2 and two FMAs from
@@ -79,30 +80,62 @@ DenseBwdPlan dense_bwd_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t 
 }
 
 // ---------------------------------------------------------------------------
-// Per row: the last visible key (min(p, N-1); -1 for padding rows and rows
-// beyond Q); per 64-row tile (one wave) its min and max.
-__global__ __launch_bounds__(256) void dense_bwd_rows_kernel(DenseArgs a, int n_qitems, int n_kitems) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  for (int64_t i = idx; i < n_qitems; i += (int64_t)gridDim.x * 256) a.q_count[i] = 0;
-  for (int64_t i = idx; i < n_kitems; i += (int64_t)gridDim.x * 256) a.k_count[i] = 0;
-  // B*Qp is a multiple of 64: whole waves leave together
-  if (idx >= (int64_t)a.B * a.Qp) return;
-  const int bi = (int)(idx / a.Qp), row = (int)(idx % a.Qp);
-  int lim = -1;
-  if (row < a.Q) {
-    const int64_t p = a.pos[(int64_t)bi * a.Q + row];
-    if (p >= 0) lim = (int)(p < a.N - 1 ? p : a.N - 1);
+// Preparation, one launch with two kinds of workgroup:
+//  * the first n_lim workgroups: per row the last visible key (min(p, N-1);
+//    -1 for padding rows and rows beyond Q), per 64-row tile (one wave) its
+//    min and max, and the split flags of both kernels cleared;
+//  * the rest: delta = dO.O and rho = dO.RC - delta*PR per (row, head),
+//    DP/8 threads per (row, head) with 16-byte loads of dO and O and two of
+//    RC (st/ops/kernels/dense.py:89-100).
+template <typename T, int DP>
+__global__ __launch_bounds__(256) void dense_bwd_prep_kernel(DenseArgs a, int n_lim, int n_qitems, int n_kitems) {
+  if ((int)blockIdx.x < n_lim) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    for (int64_t i = idx; i < n_qitems; i += (int64_t)n_lim * 256) a.q_count[i] = 0;
+    for (int64_t i = idx; i < n_kitems; i += (int64_t)n_lim * 256) a.k_count[i] = 0;
+    // B*Qp is a multiple of 64: whole waves leave together
+    if (idx >= (int64_t)a.B * a.Qp) return;
+    const int bi = (int)(idx / a.Qp), row = (int)(idx % a.Qp);
+    int lim = -1;
+    if (row < a.Q) {
+      const int64_t p = a.pos[(int64_t)bi * a.Q + row];
+      if (p >= 0) lim = (int)(p < a.N - 1 ? p : a.N - 1);
+    }
+    a.lim[idx] = lim;
+    const int mx = wave_max(lim), mn = wave_min(lim);
+    if ((threadIdx.x & 63) == 0) {
+      a.tmax[idx / kRT] = mx;
+      a.tmin[idx / kRT] = mn;
+    }
+    return;
   }
-  a.lim[idx] = lim;
-  int mx = lim, mn = lim;
+  constexpr int TR = DP / 8;  // threads per (row, head)
+  const int64_t pair = ((int64_t)blockIdx.x - n_lim) * (256 / TR) + threadIdx.x / TR;
+  const bool in = pair < (int64_t)a.B * a.Q * a.H;
+  const int c = (threadIdx.x % TR) * 8;
+  typedef T T8 __attribute__((ext_vector_type(8)));
+  float dsum = 0.f, rsum = 0.f;
+  if (in) {
+    const int64_t e = pair * DP + c;
+    const T8 g = *reinterpret_cast<const T8*>(reinterpret_cast<const T*>(a.dout) + e);
+    const T8 o = *reinterpret_cast<const T8*>(reinterpret_cast<const T*>(a.out) + e);
+    const f32x4 r0 = *reinterpret_cast<const f32x4*>(a.rc + e);
+    const f32x4 r1 = *reinterpret_cast<const f32x4*>(a.rc + e + 4);
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    mx = max(mx, __shfl_xor(mx, off, 64));
-    mn = min(mn, __shfl_xor(mn, off, 64));
+    for (int j = 0; j < 8; ++j) {
+      const float gv = to_float<T>(g[j]);
+      dsum += gv * to_float<T>(o[j]);
+      rsum += gv * (j < 4 ? r0[j] : r1[j - 4]);
+    }
   }
-  if ((threadIdx.x & 63) == 0) {
-    a.tmax[idx / kRT] = mx;
-    a.tmin[idx / kRT] = mn;
+#pragma unroll
+  for (int off = TR / 2; off > 0; off >>= 1) {
+    dsum += __shfl_xor(dsum, off, 64);
+    rsum += __shfl_xor(rsum, off, 64);
+  }
+  if (in && c == 0) {
+    a.delta[pair] = dsum;
+    a.rho[pair] = rsum - dsum * a.pr[pair];
   }
 }
 
@@ -679,7 +712,10 @@ static hipError_t launch_fast(const DenseArgs& a, hipStream_t stream) {
   const int n_ktiles = (a.N + kKT - 1) / kKT;
   const int n_rtiles = a.Qp / kRT;
   const unsigned BH = (unsigned)(a.B * a.H);
-  hipLaunchKernelGGL(dense_bwd_rows_kernel, dim3((n_rows + 255) / 256), dim3(256), 0, stream, a,
+  const int n_lim = (n_rows + 255) / 256;
+  const int64_t pairs = (int64_t)a.B * a.Q * a.H;
+  const int n_pre = (int)((pairs + 256 / (DP / 8) - 1) / (256 / (DP / 8)));
+  hipLaunchKernelGGL((dense_bwd_prep_kernel<T, DP>), dim3(n_lim + n_pre), dim3(256), 0, stream, a, n_lim,
                      (int)(n_qtiles * BH), (int)(n_ktiles * BH));
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
