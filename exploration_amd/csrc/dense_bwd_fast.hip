@@ -52,7 +52,9 @@ DenseBwdPlan dense_bwd_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t 
   const size_t rows = align256(sizeof(float) * (size_t)(B * Q * H));
   p.off_rho = rows;
   p.total = 2 * rows;
-  const bool shape_ok = (dtype == kBF16 || dtype == kF16) && (D == 64 || D == 128) && block <= kKT;
+  // 32-bit buffer offsets within one batch's K/V and Q/dO
+  const bool shape_ok = (dtype == kBF16 || dtype == kF16) && (D == 64 || D == 128) && block <= kKT &&
+                        N * H * D * 2 < (int64_t(1) << 31) && Q * H * D * 2 < (int64_t(1) << 31);
   if (!shape_ok) return p;
   const int64_t Qp = (Q + kRT - 1) / kRT * kRT;
   const int64_t n_rtiles = Qp / kRT;
@@ -228,10 +230,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const T* kg = reinterpret_cast<const T*>(a.k) + ((int64_t)bi * N * H + hh) * D;
   const T* vg = reinterpret_cast<const T*>(a.v) + ((int64_t)bi * N * H + hh) * D;
   const int64_t kstride = H * D;
-  const Stager<T, DP, WAVES> stager(kstride);
+  const Stager<T, DP, WAVES> kst(kg, kstride, a.N), vst(vg, kstride, a.N);
   auto stage = [&]<int BUF>(int i) {
-    stager.template stage<NT>(BUF ? k1s : k0s, kg, kstride, i * NT, a.N);
-    stager.template stage<NT>(BUF ? v1s : v0s, vg, kstride, i * NT, a.N);
+    kst.template stage<NT>(BUF ? k1s : k0s, i * NT);
+    vst.template stage<NT>(BUF ? v1s : v0s, i * NT);
   };
   if (t1 > t0) stage.template operator()<0>(t0);
 
@@ -499,11 +501,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const T* gg = reinterpret_cast<const T*>(a.dout) + ((int64_t)bi * a.Q * H + hh) * D;
   const float2* tg = a.tab + ((int64_t)bh * a.nblk + (int64_t)kt_idx * NB) * a.Qp;
   const int* lg = a.lim + (int64_t)bi * a.Qp;
-  const Stager<T, DP, WAVES> stager(kstride);
+  const Stager<T, DP, WAVES> qst(qg, kstride, a.Q), gst(gg, kstride, a.Q);
   auto stage = [&]<int BUF>(int idx) {
     const int m0 = (list[idx] >> 1) * MQ;
-    stager.template stage<MQ>(BUF ? q1s : q0s, qg, kstride, m0, a.Q);
-    stager.template stage<MQ>(BUF ? g1s : g0s, gg, kstride, m0, a.Q);
+    qst.template stage<MQ>(BUF ? q1s : q0s, m0);
+    gst.template stage<MQ>(BUF ? g1s : g0s, m0);
     // table slice: NB blocks x 64 rows of (beta, eps), 512 contiguous bytes
     // per block; 16 bytes (two rows) per lane
     char* tl = reinterpret_cast<char*>(BUF ? t1s : t0s);

@@ -117,6 +117,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       rg2 = max(rg2, range[k][2][w]);
       rg3 = min(rg3, range[k][3][w]);
     }
+    // uniform by construction; in SGPRs, everything derived from them (tile
+    // indices, loop bounds, staging addresses) stays scalar
+    rg0 = __builtin_amdgcn_readfirstlane(rg0);
+    rg1 = __builtin_amdgcn_readfirstlane(rg1);
+    rg2 = __builtin_amdgcn_readfirstlane(rg2);
+    rg3 = __builtin_amdgcn_readfirstlane(rg3);
     TileKeys t;
     // remote tiles ending at or below every valid row's remote limit need
     // no masks (padding rows are zeroed when the row is finalised)
@@ -164,7 +170,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const T* kg = reinterpret_cast<const T*>(a.k) + ((int64_t)bi * N * H + hh) * D;
   const T* vg = reinterpret_cast<const T*>(a.v) + ((int64_t)bi * N * H + hh) * D;
   const int64_t kstride = H * D;
-  const Stager<T, DP, WAVES> stager(kstride);
+  const Stager<T, DP, WAVES> kst(kg, kstride, a.N), vst(vg, kstride, a.N);
 
   Frag qf[NKC];
   {
@@ -356,8 +362,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const bool remote = MASKED ? i < n_remote : true;
     wait_vm();
     __syncthreads();
-    if (i + 2 < total) stager.template stage<NT>(PAR ? k1s : k0s, kg, kstride, tile_of(i + 2) * NT, a.N);
-    stager.template stage<NT>(PAR ? v1s : v0s, vg, kstride, tile_of(i) * NT, a.N);
+    if (i + 2 < total) kst.template stage<NT>(PAR ? k1s : k0s, tile_of(i + 2) * NT);
+    vst.template stage<NT>(PAR ? v1s : v0s, tile_of(i) * NT);
     const T* kt = PAR ? k0s : k1s;
     const T* vt = PAR ? v0s : v1s;
     const int kb = tile_of(i) * NT;
@@ -421,9 +427,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   if (total > 0) {
     // prologue: K of tiles 0 and 1, finite filler in the V buffer iteration 0
     // reads, then the S^T products of tile 0
-    stager.template stage<NT>(k0s, kg, kstride, tile_of(0) * NT, a.N);
-    stager.template stage<NT>(v1s, vg, kstride, tile_of(0) * NT, a.N);
-    if (total > 1) stager.template stage<NT>(k1s, kg, kstride, tile_of(1) * NT, a.N);
+    kst.template stage<NT>(k0s, tile_of(0) * NT);
+    vst.template stage<NT>(v1s, tile_of(0) * NT);
+    if (total > 1) kst.template stage<NT>(k1s, tile_of(1) * NT);
     wait_vm();
     __syncthreads();
 #pragma unroll
@@ -683,7 +689,7 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 DenseFwdPlan dense_fwd_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t H, int64_t D) {
   DenseFwdPlan p = {};
-  p.fast = (dtype == kBF16 || dtype == kF16) && (D == 64 || D == 128);
+  p.fast = (dtype == kBF16 || dtype == kF16) && (D == 64 || D == 128) && N * H * D * 2 < (int64_t(1) << 31);
   if (!p.fast) return p;
   p.n_qtiles = (int)((Q + 127) / 128);
   const int64_t n_ktiles = (N + 127) / 128;
@@ -698,7 +704,9 @@ DenseFwdPlan dense_fwd_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t 
 }
 
 bool dense_fwd_fast_supported(int dtype, const DenseArgs& a) {
-  return (dtype == kBF16 || dtype == kF16) && (a.D == 64 || a.D == 128);
+  // 32-bit buffer offsets within one batch's K/V
+  return (dtype == kBF16 || dtype == kF16) && (a.D == 64 || a.D == 128) &&
+         (int64_t)a.N * a.H * a.D * 2 < (int64_t(1) << 31);
 }
 
 hipError_t launch_dense_fwd_fast(int dtype, const DenseArgs& a, hipStream_t stream) {

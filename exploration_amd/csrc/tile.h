@@ -245,47 +245,54 @@ template <int DP> __device__ __forceinline__ int swz(int r) {
 constexpr int kSwzPeriod = 16;  // swz(r + 16) == swz(r)
 
 // Asynchronous copies of full-width row tiles (rows [r0, r0+ROWS) x [0, DP)
-// of a [*, stride] matrix with DP columns) into the swizzled LDS layout. One
-// instruction of the NWAVES waves moves a slab of RPI rows, and a lane's
+// of a [nrows, stride] matrix with DP columns) into the swizzled LDS layout.
+// One instruction of the NWAVES waves moves a slab of RPI rows, and a lane's
 // position within a slab (row, swizzled chunk) is the same for every slab, so
-// its byte offset is computed once: a slab inside the matrix is a wave-uniform
-// base address plus that 32-bit offset. In a slab that crosses row nrows the
-// rows at or beyond it re-read row nrows-1 (finite data whose products are
-// masked or discarded). Every wave of the workgroup takes part.
+// each copy's address is the matrix base plus a 32-bit byte offset: the
+// lane's fixed offset plus the slab's (32-bit arithmetic only, whether the
+// compiler keeps the uniform parts in scalar or vector registers). In a slab
+// that crosses row nrows the rows at or beyond it re-read row nrows-1 (finite
+// data whose products are masked or discarded). Every wave of the workgroup
+// takes part. The host keeps nrows * stride * sizeof(T) below 2^31.
 template <typename T, int DP, int NWAVES> struct Stager {
   static_assert(sizeof(T) == 2, "16-bit tiles");
   static constexpr int CPR = DP / 8;                // 16-byte chunks per row
   static constexpr int RPI = NWAVES * 64 / CPR;     // rows per slab
   static_assert(RPI % kSwzPeriod == 0, "a slab must keep the swizzle phase");
-  int r_lane, chunk;
-  uint32_t off;
-  __device__ __forceinline__ explicit Stager(int64_t stride) {
+  const char* base;
+  uint32_t row_bytes;
+  int nrows, r_lane;
+  uint32_t voff;  // r_lane * row_bytes + 16 * swizzled chunk
+  __device__ __forceinline__ Stager(const T* base_, int64_t stride, int nrows_) {
     const int p = (int)threadIdx.x;
     r_lane = p / CPR;
-    chunk = (p % CPR) ^ swz<DP>(r_lane);
-    off = (uint32_t)(((int64_t)r_lane * stride + chunk * 8) * (int64_t)sizeof(T));
+    const int chunk = (p % CPR) ^ swz<DP>(r_lane);
+    base = reinterpret_cast<const char*>(base_);
+    row_bytes = (uint32_t)(stride * (int64_t)sizeof(T));
+    nrows = nrows_;
+    voff = (uint32_t)r_lane * row_bytes + (uint32_t)chunk * 16u;
   }
   template <int ROWS>
-  __device__ __forceinline__ void stage(T* lds, const T* g, int64_t stride, int r0, int nrows) const {
+  __device__ __forceinline__ void stage(T* lds, int r0) const {
     static_assert(ROWS % RPI == 0, "tile must split into whole slabs");
     // wave-uniform (scalar) so that the LDS destinations are scalar too
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (r0 + ROWS <= nrows) {
+      const uint32_t s0 = (uint32_t)r0 * row_bytes, slab = (uint32_t)RPI * row_bytes;
 #pragma unroll
-      for (int it = 0; it < ROWS / RPI; ++it) {
-        const char* base = reinterpret_cast<const char*>(g + (int64_t)(r0 + it * RPI) * stride);
-        async_copy16(base + off, lds + (it * NWAVES + wave) * 64 * 8);
-      }
+      for (int it = 0; it < ROWS / RPI; ++it)
+        async_copy16(base + (voff + (s0 + (uint32_t)it * slab)), lds + (it * NWAVES + wave) * 64 * 8);
     } else {
       // recomputed per call: hoisting r_lane + it*RPI out of the caller's
       // loop would hold (or spill) one register per slab
       int rl = r_lane;
       __asm__ volatile("" : "+v"(rl));
+      const uint32_t cb = voff - (uint32_t)r_lane * row_bytes;
 #pragma unroll
       for (int it = 0; it < ROWS / RPI; ++it) {
         int row = r0 + it * RPI + rl;
         row = row < nrows ? row : nrows - 1;
-        async_copy16(g + (int64_t)row * stride + chunk * 8, lds + (it * NWAVES + wave) * 64 * 8);
+        async_copy16(base + ((uint32_t)row * row_bytes + cb), lds + (it * NWAVES + wave) * 64 * 8);
       }
     }
   }
