@@ -35,6 +35,8 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
     p.add_argument("--no-sparse", action="store_true", help="skip the cfg4 sparse measurement")
     p.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU baseline sample")
+    p.add_argument("--no-model", action="store_true", help="skip the cfg5 Stack model training step")
+    p.add_argument("--model-steps", type=int, default=20, help="timed cfg5 training steps")
     return p.parse_args()
 
 
@@ -119,6 +121,35 @@ def bench_sparse(args, torch, device):
             "bytes": nbytes, "scan_bytes": scan_bytes, "gbs": gbs, "ids_exact": exact}
 
 
+def bench_model(args, torch, device):
+    """cfg5: one training step of a stack_100m-shaped model (random init, bf16
+    autocast, AdamW, checkpointed chunks) on uniform token ids, batch 1,
+    length 8192, every position supervised; tokens/s over the timed steps
+    (the reference engine's figure, st/runtime/engine.py:192)."""
+    from exploration_amd.model import STACK_100M, build_model
+    from exploration_amd.train import check_step, make_optimizer, synthetic_lm_batch, train_step
+
+    length = 8192
+    model = build_model(STACK_100M, execution={"checkpoint_chunks": True}, device=device)
+    opt = make_optimizer(model)
+    ids, targets = synthetic_lm_batch(STACK_100M["vocab_size"], length, batch=1, seed=0, device=device)
+    losses = []
+
+    def step():
+        losses.append(train_step(model, opt, ids, targets)[0])
+
+    per, wall = timed_steps(step, 3, args.model_steps, torch)
+    loss, _, count = train_step(model, opt, ids, targets)
+    check_step(loss, count)
+    ms = sum(per) / len(per)
+    chunk = model._chunk_size(length)
+    return {"tokens_per_s": length / (ms * 1e-3), "ms_mean": ms, "ms_median": statistics.median(per),
+            "wall_s": wall, "steps": args.model_steps, "warmup": 3,
+            "params": sum(p.numel() for p in model.parameters()),
+            "dense_calls_per_step": -(-(length - 1) // chunk), "query_chunk": chunk,
+            "loss_first": float(losses[0]), "loss_last": float(loss)}
+
+
 def cpu_baseline(budget_s, torch):
     """The oracle's eager dense forward+backward (the reference's CPU eager
     path, st/tools/benchmark.py:27-43) on a bounded sample of cfg2: one of the
@@ -164,6 +195,7 @@ def main():
     torch.cuda.set_device(device)
     dense = bench_dense(args, torch, device)
     sparse = None if args.no_sparse else bench_sparse(args, torch, device)
+    model = None if args.no_model else bench_model(args, torch, device)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds, torch)
     line = {
         "metric": METRIC, "value": round(dense["tflops"], 3), "unit": "TFLOP/s", "n_gpus": 1,
@@ -192,6 +224,14 @@ def main():
                          "unit": "GB/s", "frac": round(sparse["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
                          "algorithmic_bytes": sparse["bytes"]},
             **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in sparse.items()},
+        }
+    if model is not None:
+        line["cfg5"] = {
+            "workload": "cfg5: stack_100m-shaped model (vocab 256, dim 1024, H16 D64, b16, arch Lx7,G, ffn 4.0), "
+                        "random init, bf16 autocast, AdamW, batch 1, length 8192, uniform token ids, next-token "
+                        "targets at every position",
+            "metric": "training tokens/s", "value": round(model["tokens_per_s"], 1), "unit": "tokens/s",
+            **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in model.items()},
         }
     print(json.dumps(line), flush=True)
 
