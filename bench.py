@@ -143,11 +143,42 @@ def bench_model(args, torch, device):
     check_step(loss, count)
     ms = sum(per) / len(per)
     chunk = model._chunk_size(length)
-    return {"tokens_per_s": length / (ms * 1e-3), "ms_mean": ms, "ms_median": statistics.median(per),
-            "wall_s": wall, "steps": args.model_steps, "warmup": 3,
-            "params": sum(p.numel() for p in model.parameters()),
-            "dense_calls_per_step": -(-(length - 1) // chunk), "query_chunk": chunk,
-            "loss_first": float(losses[0]), "loss_last": float(loss)}
+    result = {"tokens_per_s": length / (ms * 1e-3), "ms_mean": ms, "ms_median": statistics.median(per),
+              "wall_s": wall, "steps": args.model_steps, "warmup": 3,
+              "params": sum(p.numel() for p in model.parameters()),
+              "dense_calls_per_step": -(-(length - 1) // chunk), "query_chunk": chunk,
+              "loss_first": float(losses[0]), "loss_last": float(loss)}
+    del opt
+    result["decode"] = bench_decode(model, torch)
+    return result
+
+
+def bench_decode(model, torch, context=131072, queries=16):
+    """cfg5 tail: the trained model in bf16, streaming prefill of a 131,072-token
+    prompt into an HBM page cache, then the sparse read (top-64 of 8,192
+    blocks) for the 16 tail positions; decode = one iter_logits pass."""
+    from exploration_amd.inference import InferenceSession
+    from exploration_amd.train import synthetic_lm_batch
+
+    model = model.to(torch.bfloat16).eval()
+    ids, _ = synthetic_lm_batch(model.lm_head.out_features, context, batch=1, seed=1)
+    positions = torch.arange(context - queries, context)[None]
+    with InferenceSession(model) as session:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        session.prefill(ids, positions)
+        torch.cuda.synchronize()
+        prefill_s = time.perf_counter() - t0
+
+        def decode():
+            for _ in session.iter_logits():
+                pass
+
+        per, _ = timed_steps(decode, 2, 10, torch)
+        plan = session.plan.to_dict()
+    return {"context": context, "queries": queries, "topk": model.topk, "cache": plan["cache"],
+            "prefill_s": prefill_s, "prefill_tokens_per_s": context / prefill_s,
+            "decode_ms_mean": sum(per) / len(per), "decode_ms_median": statistics.median(per)}
 
 
 def cpu_baseline(budget_s, torch):

@@ -15,6 +15,13 @@ KV sources:
 * ``PagedKV``: a page pool ``[P, H, page_tokens, D]`` addressed through a page
   table ``[B, pages]`` (logical page -> pool page). New in this package; it
   keeps the ``pages()`` / ``touched_pages()`` protocol of ``TensorPages``.
+* ``HostPages``: ``k, v`` in (pinned) host memory, for caches larger than HBM
+  (the reference's CPU tier, ``st/runtime/inference.py:19-43`` with the page
+  loop of ``st/ops/sparse.py:81-96,121-139``). The score scan streams K
+  through two device buffers on a copy stream while the previous chunk is
+  scored; after the selection (one host synchronisation for the touched
+  block set) the K/V blocks the read needs are copied into a block-paged
+  device pool and read through the paged kernels.
 """
 import torch
 
@@ -140,6 +147,82 @@ class PagedKV:
         return (local // self.page_tokens).unique().cpu().tolist()
 
 
+class HostPages:
+    """Host-resident raw K/V ``[B, N, H, D]`` (absolute tokens
+    ``[offset, offset + N)``) streamed to ``device`` in chunks of
+    ``chunk_tokens`` tokens. Pinned tensors make the copies asynchronous."""
+
+    def __init__(self, k, v, device, chunk_tokens=65536, offset=0):
+        if k.shape != v.shape or k.ndim != 4 or k.device.type != "cpu":
+            raise ValueError("expected host k, v [B, N, H, D]")
+        self.k, self.v, self.device = k, v, torch.device(device)
+        self.chunk_tokens = self.page_tokens = int(chunk_tokens)
+        self.offset, self.length = int(offset), k.shape[1]
+
+
+def _sparse_host(q, cache, positions, b, topk, return_selection):
+    """Scan (streamed K), selection, then the paged read of the touched blocks."""
+    lib = _lib.load()
+    if cache.k.dtype != q.dtype or cache.k.shape[0] != q.shape[0] or cache.k.shape[2:] != q.shape[2:]:
+        raise ValueError("q and the host KV cache differ in dtype or batch/head dimensions")
+    batch, queries, heads, dim = q.shape
+    n, off = cache.length, cache.offset
+    chunk = max(b, cache.chunk_tokens // b * b)
+    n_blocks = -(-n // b)
+    scores = torch.empty((batch, queries, heads, n_blocks), device=q.device, dtype=torch.float32)
+    main = torch.cuda.current_stream(q.device)
+    copier = torch.cuda.Stream(q.device)
+    copier.wait_stream(main)  # device->host writes of the cache issued on the main stream come first
+    bufs = [torch.empty(batch * min(chunk, n) * heads * dim, device=q.device, dtype=q.dtype) for _ in range(2)]
+    ready = [torch.cuda.Event() for _ in range(2)]
+    free = [torch.cuda.Event() for _ in range(2)]
+    for i, lo in enumerate(range(0, n, chunk)):
+        hi, slot = min(n, lo + chunk), i % 2
+        part = bufs[slot][:batch * (hi - lo) * heads * dim].view(batch, hi - lo, heads, dim)
+        with torch.cuda.stream(copier):
+            if i >= 2:
+                copier.wait_event(free[slot])
+            part.copy_(cache.k[:, lo:hi], non_blocking=True)
+            ready[slot].record(copier)
+        main.wait_event(ready[slot])
+        g0, g1 = lo // b, -(-hi // b)
+        scores[..., g0:g1] = block_scores(q, part, positions, b, offset=off + lo)
+        free[slot].record(main)
+    values, ids, log_zr = select_blocks(scores, topk, id_base=off // b)
+    # blocks the read touches per batch row: the selection and the two local
+    # blocks of every query (host synchronisation)
+    pos = positions.to(q.device, torch.int64)
+    local = torch.stack((pos // b - 1, pos // b), -1)[:, :, None, :].expand(batch, queries, heads, 2)
+    wanted = torch.cat((ids, local), -1).reshape(batch, -1) - off // b
+    wanted = wanted.cpu()
+    table = torch.zeros((batch, n_blocks), dtype=torch.int32)
+    rows, blocks = [], []
+    for r in range(batch):
+        w = wanted[r]
+        uniq = w[(w >= 0) & (w < n_blocks)].unique()
+        table[r, uniq] = torch.arange(len(blocks), len(blocks) + len(uniq), dtype=torch.int32)
+        rows.append(torch.full_like(uniq, r))
+        blocks.append(uniq)
+    rows, blocks = torch.cat(rows), torch.cat(blocks)
+    tok = (blocks[:, None] * b + torch.arange(b)).clamp(max=n - 1)       # [T, b]
+    pools = []
+    for src in (cache.k, cache.v):
+        staged = src[rows[:, None], tok].permute(0, 2, 1, 3).contiguous()  # [T, H, b, D]
+        pools.append(staged.pin_memory().to(q.device, non_blocking=True))
+    table = table.to(q.device, non_blocking=True)
+    ws_bytes = lib.st_sparse_workspace_bytes(batch, queries, heads, dim, topk, 0)
+    ws = torch.empty(max(ws_bytes, 256), device=q.device, dtype=torch.uint8)
+    out = torch.empty_like(q)
+    _lib.check(lib.st_sparse_pop(_lib.DTYPE_CODES[q.dtype], batch, queries, heads, dim, b, _lib.ptr(q),
+                                 _lib.ptr(pos), _lib.ptr(pools[0]), _lib.ptr(pools[1]), _lib.ptr(table), b,
+                                 n_blocks, n, off, _lib.ptr(ids), _lib.ptr(values), _lib.ptr(log_zr), topk,
+                                 _lib.ptr(out), None, _lib.ptr(ws), ws.numel(), _lib.stream_of(q)), lib)
+    _record("sparse_pop", q, b, True)
+    if return_selection:
+        return out, {"indices": ids, "scores": values, "log_zr": log_zr}
+    return out
+
+
 def _kv_view(cache, q, block_size):
     """(k, v, page_table, page_tokens, pages_per_seq, n_tokens, offset) of a
     device-resident cache, or ValueError."""
@@ -187,6 +270,9 @@ def sparse_attention(q, cache, positions, block_size, topk, backend="auto", grou
         raise ValueError("unsupported HIP sparse configuration")
     if q.ndim != 4 or positions.shape != q.shape[:2]:
         raise ValueError("expected q[B,Q,H,D], positions[B,Q]")
+    if isinstance(cache, HostPages):
+        return _sparse_host(q.contiguous(), cache, positions.to(device=q.device, dtype=torch.int64).contiguous(),
+                            b, topk, return_selection)
     lib = _lib.load()
     k, v, table, page_tokens, pages_per_seq, n_tokens, offset = _kv_view(cache, q, b)
     q = q.contiguous()
