@@ -40,6 +40,22 @@ def parse():
     return p.parse_args()
 
 
+def profiled_traffic():
+    """HBM bytes per step of the dense and sparse paths, from the calibrated
+    FETCH_SIZE/WRITE_SIZE summary committed under profiles/ (None if absent)."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_cfg2_dense_cfg4_sparse.md")
+    found = {}
+    try:
+        for line in open(path):
+            parts = line.split()
+            if len(parts) == 2 and parts[0] == "traffic" and "=" in parts[1]:
+                key, value = parts[1].split("=")
+                found[key] = int(value)
+    except OSError:
+        pass
+    return found.get("dense_step_bytes"), found.get("sparse_step_bytes")
+
+
 def timed_steps(step, warmup, steps, torch):
     for _ in range(warmup):
         step()
@@ -228,6 +244,7 @@ def main():
     sparse = None if args.no_sparse else bench_sparse(args, torch, device)
     model = None if args.no_model else bench_model(args, torch, device)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds, torch)
+    traffic = profiled_traffic()
     line = {
         "metric": METRIC, "value": round(dense["tflops"], 3), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dense["ms_mean"], 4),
@@ -237,10 +254,11 @@ def main():
                                "block 128, causal, q/k/v ~ N(0,1)/sqrt(128), dO ~ N(0,1)",
                    "global_batch": 1, "seq_len": 4096, "heads": 8, "head_dim": 128, "block_size": 128,
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "kernel": "dense forward+backward (dense_fwd, dense_bwd_pre, "
-                     "dense_bwd_dq, dense_bwd_dkv)",
+        "roofline": {"bound": "mfma", "kernel": "dense forward+backward, one step (dense_fwd_fast, "
+                     "dense_fwd_merge, dense_bwd_prep, dense_bwd_dq_fast, dense_bwd_dkv_fast, dense_bwd_merge)",
                      "achieved": round(dense["tflops"], 3), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(dense["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "frac": round(dense["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic[0],
+                     "traffic_unit": "bytes per step (calibrated FETCH_SIZE + WRITE_SIZE)",
                      "algorithmic_flop": dense["flops"]},
         "dense": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in dense.items()},
         "cpu_baseline": cpu,
@@ -252,7 +270,8 @@ def main():
             "value": round(sparse["gbs"], 2), "unit": "GB/s", "ms": round(sparse["ms_mean"], 4),
             "ids_bit_exact": sparse["ids_exact"],
             "roofline": {"bound": "hbm", "achieved": round(sparse["gbs"], 2), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(sparse["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                         "unit": "GB/s", "frac": round(sparse["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic[1],
+                         "traffic_unit": "bytes per forward (calibrated FETCH_SIZE + WRITE_SIZE)",
                          "algorithmic_bytes": sparse["bytes"]},
             **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in sparse.items()},
         }
