@@ -30,10 +30,12 @@ FLAGS = [
 ]
 
 
-# Per-source extra flags. The pipelined forward keeps its score tiles in
-# VGPRs (MFMA results feed the softmax directly, no AGPR round trip).
+# Per-source extra flags. The pipelined dense kernels keep their score tiles
+# in VGPRs (MFMA results feed the softmax directly, no AGPR round trip; for
+# the dQ kernel this also removes its scratch spills).
 EXTRA_FLAGS = {
     "dense_fwd_fast.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "dense_bwd_fast.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

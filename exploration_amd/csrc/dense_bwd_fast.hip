@@ -304,51 +304,56 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         });
     // key of register r in subtile st: kb + 4*half + off(st, r)
     const int base_k = kb + 4 * half;
-    const int lim_r = rlim - base_k;     // remote iff off < lim_r
     const int lim_v = lhi + 1 - base_k;  // visible iff off < lim_v
     auto offset = [](int st, int r) { return 32 * st + 8 * (r >> 2) + (r & 3); };
+    // Remote-ness is constant over a key block (the remote limit is block
+    // aligned), so it is one flag per block slot; only visibility (the
+    // causal limit) varies per key. Per slot: the exponent base, the
+    // multiplier P/u (U_j e^{ZR-Z} remote, 1 local) and the gate coefficient.
+    constexpr int NS = BlkSlots<LOGB>::n;
+    bool remb[NST][NS];
+    float nbase[NST][NS];
+#pragma unroll
+    for (int st = 0; st < NST; ++st)
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+        remb[st][j] = FULL || (blk_index<LOGB>(st, j, half) << LOGB) < rlim - kb;
+        nbase[st][j] = remb[st][j] ? -base_r : -base_l;
+      }
     // u
 #pragma unroll
     for (int st = 0; st < NST; ++st)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        if constexpr (FULL) {
-          s[st][r] = fast_exp2(fmaf(s[st][r], c2, -base_r));
-        } else {
-          const int off = offset(st, r);
-          const float x = fmaf(s[st][r], c2, off < lim_r ? -base_r : -base_l);
-          s[st][r] = off < lim_v ? fast_exp2(x) : 0.f;
-        }
+        const float x = fmaf(s[st][r], c2, nbase[st][blk_slot<LOGB>(r)]);
+        if constexpr (FULL) s[st][r] = fast_exp2(x);
+        else s[st][r] = offset(st, r) < lim_v ? fast_exp2(x) : 0.f;
       }
     // U_j, then direct = P (dP - delta) with P = u U_j e^{ZR-Z} (remote) or u
     float ub[NST][8];
     block_sums<NST, LOGB>(s, ub);
+    float mult[NST][NS];
 #pragma unroll
     for (int st = 0; st < NST; ++st)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float ur = ub[st][blk_slot<LOGB>(r)] * ezrz;
-        float mult;
-        if constexpr (FULL) mult = ur;
-        else mult = offset(st, r) < lim_r ? ur : 1.f;
-        dp[st][r] = s[st][r] * mult * (dp[st][r] - dl);
-      }
+      for (int j = 0; j < NS; ++j) mult[st][j] = remb[st][j] ? ub[st][j] * ezrz : 1.f;
+#pragma unroll
+    for (int st = 0; st < NST; ++st)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dp[st][r] = s[st][r] * mult[st][blk_slot<LOGB>(r)] * (dp[st][r] - dl);
     float gb[NST][8];
     block_sums<NST, LOGB>(dp, gb);
-    // gate coefficient per block: G_j / U_j - rho (0 where U_j = 0: every u is 0)
-    constexpr int NS = BlkSlots<LOGB>::n;
+    // gate coefficient per block: G_j / U_j - rho on remote blocks (0 where
+    // U_j = 0: every u is 0), 0 on local ones
 #pragma unroll
     for (int st = 0; st < NST; ++st)
 #pragma unroll
-      for (int j = 0; j < NS; ++j) gb[st][j] = ub[st][j] > 0.f ? gb[st][j] / ub[st][j] - rho : 0.f;
+      for (int j = 0; j < NS; ++j)
+        gb[st][j] = remb[st][j] && ub[st][j] > 0.f ? gb[st][j] / ub[st][j] - rho : 0.f;
 #pragma unroll
     for (int st = 0; st < NST; ++st)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float g = gb[st][blk_slot<LOGB>(r)];
-        if constexpr (FULL) dp[st][r] = fmaf(s[st][r], g, dp[st][r]);
-        else dp[st][r] = offset(st, r) < lim_r ? fmaf(s[st][r], g, dp[st][r]) : dp[st][r];
-      }
+      for (int r = 0; r < 16; ++r) dp[st][r] = fmaf(s[st][r], gb[st][blk_slot<LOGB>(r)], dp[st][r]);
     // table entries of this tile's blocks (one writer per row and block)
     if (row_in && (BlkSlots<LOGB>::per_half || half == 0)) {
       constexpr int STEP = LOGB >= 5 ? ((1 << LOGB) / 32 < NST ? (1 << LOGB) / 32 : NST) : 1;
