@@ -569,20 +569,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     f32x16 s[NRS], dp[NRS];
 #pragma unroll
     for (int rs = 0; rs < NRS; ++rs) { s[rs] = zero16(); dp[rs] = zero16(); }
-    // product j: row subtile j / (2 NKC), chunk (j / 2) % NKC, S (even j) or dP (odd j)
-    mfma_phase<NRS * 2 * NKC, 4, 1>(
-        [&](int j) { return rfrag((j & 1) ? gt : qt, j / (2 * NKC), (j >> 1) % NKC); },
-        [&](int j, Frag f) {
-          const int rs = j / (2 * NKC), c = (j >> 1) % NKC;
-          if (j & 1) dp[rs] = M::mma(f, vf[c], dp[rs]);
-          else s[rs] = M::mma(f, kf[c], s[rs]);
-        });
-    // register r of row subtile rs holds row 32rs + 8(r/4) + 4half + r%4
-#pragma unroll
-    for (int rs = 0; rs < NRS; ++rs)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r0 = 32 * rs + 8 * i + 4 * half;
+    Frag bp[NRS][2], bd[NRS][2];
+    // Elementwise work of row subtile RS, slice I: register group I (rows
+    // 32RS + 8I + 4half + 0..3) for I < 4, then the conversion of P and dA
+    // to 16-bit MFMA operands (row order permuted as in frag_from_c).
+    auto elem = [&]<int RS, int I>() {
+      if constexpr (I < 4) {
+        const int r0 = 32 * RS + 8 * I + 4 * half;
         const f32x4 t01 = *reinterpret_cast<const f32x4*>(tt + 2 * r0);
         const f32x4 t23 = *reinterpret_cast<const f32x4*>(tt + 2 * r0 + 4);
         const float beta[4] = {t01[0], t01[2], t23[0], t23[2]};
@@ -596,37 +589,57 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int r = 4 * i + j;
-          const float pv = fast_exp2(fmaf(s[rs][r], c2, -beta[j]));
-          const float da = pv * (dp[rs][r] + eps[j]);
+          const int r = 4 * I + j;
+          const float pv = fast_exp2(fmaf(s[RS][r], c2, -beta[j]));
+          const float da = pv * (dp[RS][r] + eps[j]);
           if constexpr (FULL) {
-            s[rs][r] = pv;
-            dp[rs][r] = da;
+            s[RS][r] = pv;
+            dp[RS][r] = da;
           } else {
             const bool vis = key <= lim[j];
-            s[rs][r] = vis ? pv : 0.f;
-            dp[rs][r] = vis ? da : 0.f;
+            s[RS][r] = vis ? pv : 0.f;
+            dp[RS][r] = vis ? da : 0.f;
           }
         }
-      }
-    // dV^T += dO^T P, dK^T += Q^T dA (row order permuted as in frag_from_c)
-    Frag bp[NRS][2], bd[NRS][2];
+      } else {
 #pragma unroll
-    for (int rs = 0; rs < NRS; ++rs)
-#pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        bp[rs][h2] = frag_from_c<T>(s[rs], h2);
-        bd[rs][h2] = frag_from_c<T>(dp[rs], h2);
+        for (int h2 = 0; h2 < 2; ++h2) {
+          bp[RS][h2] = frag_from_c<T>(s[RS], h2);
+          bd[RS][h2] = frag_from_c<T>(dp[RS], h2);
+        }
       }
-    // product j: 16-row chunk j / (2 NDT), head-dim tile (j / 2) % NDT,
-    // dV (even j, from dO^T) or dK (odd j, from Q^T)
-    mfma_phase<NRS * 2 * 2 * NDT, 4, 2>(
-        [&](int j) { return tfrag((j & 1) ? qt : gt, 16 * (j / (2 * NDT)), (j >> 1) % NDT); },
-        [&](int j, Frag f) {
-          const int ch = j / (2 * NDT), dt = (j >> 1) % NDT;
-          if (j & 1) dk[dt] = M::mma(f, bd[ch >> 1][ch & 1], dk[dt]);
-          else dv[dt] = M::mma(f, bp[ch >> 1][ch & 1], dv[dt]);
-        });
+    };
+    // S = Q K^T and dP = dO V^T of row subtile RS: product j is chunk j/2,
+    // S (even j) or dP (odd j)
+    auto p1_load = [&]<int RS>(int j) { return rfrag((j & 1) ? gt : qt, RS, j >> 1); };
+    auto p1_mma = [&]<int RS>(int j, Frag f) {
+      if (j & 1) dp[RS] = M::mma(f, vf[j >> 1], dp[RS]);
+      else s[RS] = M::mma(f, kf[j >> 1], s[RS]);
+    };
+    // dV^T += dO^T P and dK^T += Q^T dA over the rows of subtile RS: product
+    // j is 16-row chunk 2RS + j/(2NDT), head-dim tile (j/2) % NDT, dV (even j)
+    // or dK (odd j)
+    auto p2_load = [&]<int RS>(int j) {
+      return tfrag((j & 1) ? qt : gt, 16 * (2 * RS + j / (2 * NDT)), (j >> 1) % NDT);
+    };
+    auto p2_mma = [&]<int RS>(int j, Frag f) {
+      const int h2 = j / (2 * NDT), dt = (j >> 1) % NDT;
+      if (j & 1) dk[dt] = M::mma(f, bd[RS][h2], dk[dt]);
+      else dv[dt] = M::mma(f, bp[RS][h2], dv[dt]);
+    };
+    static_assert(NRS == 2, "two row subtiles per step");
+    // subtile 0's products; subtile 1's products overlap subtile 0's
+    // elementwise work; subtile 0's dK/dV products overlap subtile 1's
+    mfma_phase<2 * NKC, 4, 1>([&](int j) { return p1_load.template operator()<0>(j); },
+                              [&](int j, Frag f) { p1_mma.template operator()<0>(j, f); });
+    mfma_phase_overlap<2 * NKC, 4, 1, 5>([&](int j) { return p1_load.template operator()<1>(j); },
+                                         [&](int j, Frag f) { p1_mma.template operator()<1>(j, f); },
+                                         [&]<int K>() { elem.template operator()<0, K>(); });
+    mfma_phase_overlap<4 * NDT, 4, 2, 5>([&](int j) { return p2_load.template operator()<0>(j); },
+                                         [&](int j, Frag f) { p2_mma.template operator()<0>(j, f); },
+                                         [&]<int K>() { elem.template operator()<1, K>(); });
+    mfma_phase<4 * NDT, 4, 2>([&](int j) { return p2_load.template operator()<1>(j); },
+                              [&](int j, Frag f) { p2_mma.template operator()<1>(j, f); });
   };
   auto run = [&]<int BUF>(int idx) {
     if (list[idx] & 1) step.template operator()<BUF, true>(idx);

@@ -3,6 +3,8 @@
 // per-(row, key block) reductions.
 #pragma once
 
+#include <utility>
+
 #include "common.h"
 
 namespace st {
@@ -357,6 +359,38 @@ __device__ __forceinline__ void mfma_phase(Load&& load, Mfma&& mma) {
     if (g + 1 < N / L) __builtin_amdgcn_sched_group_barrier(0x100, L * R, 0);  // the reads first
     __builtin_amdgcn_sched_group_barrier(0x008, L, 0);                         // then the MFMAs
   }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// mfma_phase with independent VALU work placed between the chunks: after
+// chunk g's MFMAs, slices [g*NS/C, (g+1)*NS/C) of NS run in the same
+// scheduling region (C = N/L chunks), so one wave overlaps them with its own
+// MFMAs. slice.template operator()<k>() must not read this phase's results.
+template <int N, int L, int R, int NS, typename Load, typename Mfma, typename Slice>
+__device__ __forceinline__ void mfma_phase_overlap(Load&& load, Mfma&& mma, Slice&& slice) {
+  static_assert(N % L == 0, "phase must split into whole chunks");
+  constexpr int C = N / L;
+  typedef decltype(load(0)) F;
+  F buf[2][L];
+#pragma unroll
+  for (int i = 0; i < L; ++i) buf[0][i] = load(i);
+  [&]<int... G>(std::integer_sequence<int, G...>) {
+    ([&] {
+      constexpr int g = G;
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt untouched
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (g + 1 < C) {
+#pragma unroll
+        for (int i = 0; i < L; ++i) buf[(g + 1) & 1][i] = load((g + 1) * L + i);
+      }
+#pragma unroll
+      for (int i = 0; i < L; ++i) mma(g * L + i, buf[g & 1][i]);
+      [&]<int... K>(std::integer_sequence<int, K...>) {
+        (slice.template operator()<g * NS / C + K>(), ...);
+      }(std::make_integer_sequence<int, (g + 1) * NS / C - g * NS / C>{});
+    }(), ...);
+  }(std::make_integer_sequence<int, C>{});
   __builtin_amdgcn_sched_barrier(0);
 }
 
