@@ -294,14 +294,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     f32x16 s[NST], dp[NST];
 #pragma unroll
     for (int st = 0; st < NST; ++st) { s[st] = zero16(); dp[st] = zero16(); }
-    // product j: subtile j / (2 NKC), chunk (j / 2) % NKC, S (even j) or dP (odd j)
-    mfma_phase<NST * 2 * NKC, 4, 1>(
-        [&](int j) { return rfrag((j & 1) ? vt : kt, j / (2 * NKC), (j >> 1) % NKC); },
-        [&](int j, Frag f) {
-          const int st = j / (2 * NKC), c = (j >> 1) % NKC;
-          if (j & 1) dp[st] = M::mma(f, gf[c], dp[st]);
-          else s[st] = M::mma(f, qf[c], s[st]);
-        });
     // key of register r in subtile st: kb + 4*half + off(st, r)
     const int base_k = kb + 4 * half;
     const int lim_v = lhi + 1 - base_k;  // visible iff off < lim_v
@@ -320,15 +312,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         remb[st][j] = FULL || (blk_index<LOGB>(st, j, half) << LOGB) < rlim - kb;
         nbase[st][j] = remb[st][j] ? -base_r : -base_l;
       }
-    // u
+    // u of subtile ST, registers 8H..8H+7
+    auto expo = [&]<int ST, int H>() {
 #pragma unroll
-    for (int st = 0; st < NST; ++st)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float x = fmaf(s[st][r], c2, nbase[st][blk_slot<LOGB>(r)]);
-        if constexpr (FULL) s[st][r] = fast_exp2(x);
-        else s[st][r] = offset(st, r) < lim_v ? fast_exp2(x) : 0.f;
+      for (int r = 8 * H; r < 8 * H + 8; ++r) {
+        const float x = fmaf(s[ST][r], c2, nbase[ST][blk_slot<LOGB>(r)]);
+        if constexpr (FULL) s[ST][r] = fast_exp2(x);
+        else s[ST][r] = offset(ST, r) < lim_v ? fast_exp2(x) : 0.f;
       }
+    };
+    // S^T = K Q^T and dP^T = V dO^T of subtile ST: product j is chunk j/2,
+    // S (even j) or dP (odd j); the exponentials of subtile ST-1 overlap them
+    auto p1 = [&]<int ST>() {
+      auto load = [&](int j) { return rfrag((j & 1) ? vt : kt, ST, j >> 1); };
+      auto mma = [&](int j, Frag f) {
+        if (j & 1) dp[ST] = M::mma(f, gf[j >> 1], dp[ST]);
+        else s[ST] = M::mma(f, qf[j >> 1], s[ST]);
+      };
+      if constexpr (ST == 0) mfma_phase<2 * NKC, 4, 1>(load, mma);
+      else mfma_phase_overlap<2 * NKC, 4, 1, 2>(load, mma, [&]<int K>() { expo.template operator()<ST - 1, K>(); });
+    };
+    [&]<int... ST>(std::integer_sequence<int, ST...>) {
+      (p1.template operator()<ST>(), ...);
+    }(std::make_integer_sequence<int, NST>{});
+    expo.template operator()<NST - 1, 0>();
+    expo.template operator()<NST - 1, 1>();
     // U_j, then direct = P (dP - delta) with P = u U_j e^{ZR-Z} (remote) or u
     float ub[NST][8];
     block_sums<NST, LOGB>(s, ub);
@@ -350,10 +358,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
       for (int j = 0; j < NS; ++j)
         gb[st][j] = remb[st][j] && ub[st][j] > 0.f ? gb[st][j] / ub[st][j] - rho : 0.f;
-#pragma unroll
-    for (int st = 0; st < NST; ++st)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) dp[st][r] = fmaf(s[st][r], gb[st][blk_slot<LOGB>(r)], dp[st][r]);
     // table entries of this tile's blocks (one writer per row and block)
     if (row_in && (BlkSlots<LOGB>::per_half || half == 0)) {
       constexpr int STEP = LOGB >= 5 ? ((1 << LOGB) / 32 < NST ? (1 << LOGB) / 32 : NST) : 1;
@@ -381,16 +385,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
           tab[(int64_t)bl * a.Qp + row] = make_float2(beta, eps);
         }
     }
-    // dQ^T += K^T dA^T
+    // dA of subtile ST (direct + gate term) as 16-bit MFMA operands
     Frag bd[NST][2];
+    auto gate = [&]<int ST>() {
 #pragma unroll
-    for (int st = 0; st < NST; ++st)
+      for (int r = 0; r < 16; ++r) dp[ST][r] = fmaf(s[ST][r], gb[ST][blk_slot<LOGB>(r)], dp[ST][r]);
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) bd[st][h2] = frag_from_c<T>(dp[st], h2);
-    // product j: 16-key chunk j / NDT, head-dim tile j % NDT
-    mfma_phase<NST * 2 * NDT, 4, 2>(
-        [&](int j) { return tfrag(kt, 16 * (j / NDT), j % NDT); },
-        [&](int j, Frag f) { acc[j % NDT] = M::mma(f, bd[j / (2 * NDT)][(j / NDT) & 1], acc[j % NDT]); });
+      for (int h2 = 0; h2 < 2; ++h2) bd[ST][h2] = frag_from_c<T>(dp[ST], h2);
+    };
+    // dQ^T += K^T dA^T over the keys of subtile ST: product j is 16-key chunk
+    // 2ST + j/NDT, head-dim tile j % NDT; subtile ST+1's gate overlaps them
+    auto p2 = [&]<int ST>() {
+      auto load = [&](int j) { return tfrag(kt, 16 * (2 * ST + j / NDT), j % NDT); };
+      auto mma = [&](int j, Frag f) { acc[j % NDT] = M::mma(f, bd[ST][j / NDT], acc[j % NDT]); };
+      if constexpr (ST + 1 < NST) mfma_phase_overlap<2 * NDT, 4, 2, 1>(load, mma, [&]<int K>() { gate.template operator()<ST + 1>(); });
+      else mfma_phase<2 * NDT, 4, 2>(load, mma);
+    };
+    gate.template operator()<0>();
+    [&]<int... ST>(std::integer_sequence<int, ST...>) {
+      (p2.template operator()<ST>(), ...);
+    }(std::make_integer_sequence<int, NST>{});
   };
   auto run = [&]<int BUF>(int i) {
     if (i < full) step.template operator()<BUF, true>(i);
