@@ -17,6 +17,11 @@
 
 namespace st {
 
+// Cost of splitting a row tile into two pieces, in key tiles (~2.8 us each
+// at D=128): the second workgroup's prologue and epilogue, its dispatch, and
+// the merge.
+constexpr int kPieceCost = 3;
+
 template <typename T, int DP, int LOGB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void dense_fwd_fast_kernel(DenseArgs a, int n_qtiles) {
   typedef Mma<T> M;
@@ -49,31 +54,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // Slot mode: 2 n_qtiles slots per head, slot k < n_qtiles takes kind 0 of
   // row tile n_qtiles-1-k, slot n_qtiles+k kind 1 of it (longest causal rows
   // first). Pair mode: row tiles L = n-1-j and S = j form pair j; slot j
-  // (j < n/2) takes kind 0 of L, slot n/2+j kind 1 of L, then an odd middle
-  // tile, then the S tiles whole, longest first. L is cut so that, under
-  // causal positions, its second piece plus S matches its first piece: the
-  // dispatcher hands each S tile to the compute unit that finishes first,
-  // which is the one that ran the short second piece of the same pair.
-  int qt, kind, partner = -1;
-  if (a.f_pair) {
-    const int P = n_qtiles / 2, odd = n_qtiles & 1;
-    if (slot < 2 * P) {
-      const int j = slot < P ? slot : slot - P;
-      qt = n_qtiles - 1 - j;
-      kind = slot >= P;
-      partner = j;
-    } else if (slot < 2 * P + odd) {
-      qt = P;
-      kind = 2;
-    } else {
-      qt = 3 * P + odd - 1 - slot;
-      kind = 2;
-    }
-  } else {
-    kind = slot >= n_qtiles;
-    qt = n_qtiles - 1 - (kind ? slot - n_qtiles : slot);
-  }
-
+  // (j < n/2) takes L whole or its first piece, slot n/2+j takes S whole;
+  // after an odd middle tile, slot 2(n/2)+odd+j takes L's second piece if L
+  // is split, else nothing. L is split only where its second piece plus S,
+  // plus the cost of the extra piece, stays below L whole; the second pieces
+  // (longest first) then go to the compute units that finish S first.
   // Per lane: the row's remote limit and local window [llo, lhi] for row
   // tile qt.
   struct RowKeys {
@@ -133,33 +118,63 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     return t;
   };
 
+  int qt, kind;
+  bool split = false;  // this job is a piece of a split row tile
+  int hsplit = 0;      // remote tiles of a split tile's first piece
+  TileKeys tk;
+  const bool middle = a.f_pair && (n_qtiles & 1) && slot == 2 * (n_qtiles / 2);
+  if (a.f_pair && !middle) {
+    // pair j: both tiles' key ranges decide whether L is split (the same
+    // decision in all three workgroups of the pair); a piece boundary
+    // (second workgroup start, epilogue, merge) counts as kPieceCost tiles
+    const int P = n_qtiles / 2, odd = n_qtiles & 1;
+    const int j = slot < P ? slot : (slot < 2 * P ? slot - P : slot - 2 * P - odd);
+    const int L = n_qtiles - 1 - j;
+    const TileKeys tl = tile_keys(row_keys(L), 0), ts = tile_keys(row_keys(j), 1);
+    const int cL = tl.n_remote_all + tl.n_local, cS = ts.n_remote_all + ts.n_local;
+    const int h = min(tl.n_remote_all, (cL + cS + kPieceCost + 1) / 2);
+    const bool sp = a.fw0 != nullptr && h > 0 && h < cL && max(h, cL - h + cS + kPieceCost) < cL;
+    if (slot < P) {
+      qt = L;  // L whole, or its first piece
+      kind = 0;
+    } else if (slot < 2 * P) {
+      qt = j;  // S whole
+      kind = 2;
+    } else {
+      if (!sp) return;  // L ran whole
+      qt = L;  // L's second piece
+      kind = 1;
+    }
+    split = sp && qt == L;
+    hsplit = h;
+    tk = qt == L ? tl : ts;
+  } else {
+    if (a.f_pair) {
+      qt = n_qtiles / 2;  // odd middle tile
+      kind = 2;
+    } else {
+      kind = slot >= n_qtiles;
+      qt = n_qtiles - 1 - (kind ? slot - n_qtiles : slot);
+    }
+    tk = tile_keys(row_keys(qt), 0);
+    const int n_all = tk.n_remote_all + tk.n_local;
+    if (a.fw0 != nullptr && kind != 2 && n_all > a.f_split) {
+      split = true;
+      hsplit = min((n_all + 1) / 2, tk.n_remote_all);
+    }
+    if (kind == 1 && !split) return;  // whole workgroup
+  }
   const int row = qt * 32 * WAVES + wave * 32 + col;
   const bool row_in = row < a.Q;
   const RowKeys rk = row_keys(qt);
   const int64_t p = rk.p;
   const int rlim = rk.rlim, llo = rk.llo, lhi = rk.lhi;
-  const TileKeys tk = tile_keys(rk, 0);
   const int full_remote = tk.full_remote, n_remote_all = tk.n_remote_all, lt0 = tk.lt0, n_local = tk.n_local;
-  const int n_all = n_remote_all + n_local;
   // A split row tile runs as two pieces: piece 0 takes remote tiles [0, h),
   // piece 1 remote tiles [h, n_remote_all) and the local tiles;
   // dense_fwd_merge combines their partial results.
-  bool split = false;
-  int hsplit = n_remote_all;
-  if (a.fw0 != nullptr && kind != 2) {
-    if (a.f_pair) {
-      // equal shares of the pair's key tiles (identical in both workgroups)
-      const TileKeys to = tile_keys(row_keys(partner), 1);
-      hsplit = min(n_remote_all, (n_all + to.n_remote_all + to.n_local + 1) / 2);
-      split = hsplit > 0 && hsplit < n_all;
-    } else if (n_all > a.f_split) {
-      split = true;
-      hsplit = min((n_all + 1) / 2, n_remote_all);
-    }
-    if (!split) hsplit = n_remote_all;
-  }
+  if (!split) hsplit = n_remote_all;
   const int piece = kind == 1;
-  if (piece && !split) return;  // whole workgroup
   const int item = bh * n_qtiles + qt;
   const int rs = piece ? hsplit : 0;                              // first remote tile of this piece
   const int n_remote = piece ? n_remote_all - hsplit : hsplit;    // remote tiles of this piece

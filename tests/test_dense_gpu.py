@@ -137,6 +137,23 @@ def test_cfg2_full_size(device):
     _check_dense(q, k, v, pos, do, b, device, torch.bfloat16, oracle_device=device, label="cfg2")
 
 
+@pytest.mark.parametrize("d,b,tiles", [(64, 64, 33), (128, 128, 32), (128, 16, 34)])
+def test_causal_pair_mode(device, d, b, tiles):
+    """Causal rows over enough 128-row tiles (B1 H8) that the forward pairs
+    row tiles n-1-j and j across workgroups, splitting some long tiles: odd
+    and even tile counts, with and without splits (oracle in float32 on the
+    GPU)."""
+    print(f"dense pair mode d={d} b={b} tiles={tiles}", flush=True)
+    n = 128 * tiles
+    g = torch.Generator().manual_seed(21 + tiles)
+    q = (torch.randn(1, n, 8, d, generator=g) / math.sqrt(d)).to(torch.bfloat16)
+    k = (torch.randn(1, n, 8, d, generator=g) / math.sqrt(d)).to(torch.bfloat16)
+    v = torch.randn(1, n, 8, d, generator=g).to(torch.bfloat16)
+    probe = torch.randn(1, n, 8, d, generator=g).to(torch.bfloat16)
+    pos = torch.arange(n)[None]
+    _check_dense(q, k, v, pos, probe, b, device, torch.bfloat16, oracle_device=device, label=f"pair{tiles}")
+
+
 def test_native_library_is_the_path(device):
     """The kernels ran from the in-tree library, bound to torch's HIP runtime."""
     q = torch.randn(1, 8, 1, 64, device=device)
