@@ -18,9 +18,10 @@
 namespace st {
 
 // Cost of splitting a row tile into two pieces, in key tiles (~2.8 us each
-// at D=128): the second workgroup's prologue and epilogue, its dispatch, and
-// the merge.
-constexpr int kPieceCost = 3;
+// at D=128): the second workgroup's dispatch, prologue, first (cold) tiles
+// and epilogue, and the merge. Measured on cfg2 over 1..8 and "never": 6 is
+// the fastest (78 us against 88 at 3 and 98 never splitting).
+constexpr int kPieceCost = 6;
 
 template <typename T, int DP, int LOGB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void dense_fwd_fast_kernel(DenseArgs a, int n_qtiles) {
