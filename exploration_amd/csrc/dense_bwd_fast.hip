@@ -37,6 +37,10 @@ namespace st {
 namespace {
 
 constexpr int kKT = 128;       // keys per dK/dV workgroup and per dQ key tile
+// Cost, in key tiles, of splitting a dQ row tile into two pieces (the second
+// workgroup's dispatch, prologue and cold first tiles, the partial's store
+// and merge).
+constexpr int kQPieceCost = 6;
 constexpr int kRT = 64;        // query rows per dK/dV step / row-tile statistic
 constexpr int kMaxRTiles = 2048;
 constexpr size_t kMaxTable = size_t(4) << 30;
@@ -175,20 +179,89 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   __shared__ __attribute__((aligned(16))) T k1s[TILE];
   __shared__ __attribute__((aligned(16))) T v0s[TILE];
   __shared__ __attribute__((aligned(16))) T v1s[TILE];
-  __shared__ int range[2][WAVES];
+  __shared__ int range[2][2][WAVES];  // two row tiles: this one and the pair partner
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 31, half = lane >> 5;
   const int BH = a.B * a.H;
-  const int bh = blockIdx.x % BH;
-  // all first pieces (longest causal rows first), then all second pieces
-  const int kq = (int)(blockIdx.x / BH);
-  const int piece = kq >= n_qtiles;
-  const int qt = n_qtiles - 1 - (piece ? kq - n_qtiles : kq);
+  const int bh = blockIdx.x % BH, slot = (int)(blockIdx.x / BH);
   const int bi = bh / a.H, hh = bh % a.H;
+  const int64_t H = a.H, D = a.D, N = a.N;
+
+  // Key tiles of row tile qt (LDS slot k, one barrier): the count up to the
+  // last visible key of any row, and how many lie below every row's remote
+  // limit (all keys remote, no masks).
+  auto tile_range = [&](int qt, int k, int& n_tiles, int& full) {
+    const int row = qt * 32 * WAVES + wave * 32 + col;
+    const int64_t p = row < a.Q ? a.pos[(int64_t)bi * a.Q + row] : -1;
+    int rl = 0, lh = -1;
+    if (p >= 0) {
+      const int64_t c = p >> LOGB;
+      const int64_t lo = (c - 1) * b > 0 ? (c - 1) * b : 0;
+      rl = (int)(lo < N ? lo : N);
+      lh = (int)(p < N - 1 ? p : N - 1);
+    }
+    const int r0 = wave_max(lh), r1 = wave_min(lh >= 0 ? rl : 0x7fffffff);
+    if (lane == 0) { range[k][0][wave] = r0; range[k][1][wave] = r1; }
+    __syncthreads();
+    int rg0 = range[k][0][0], rg1 = range[k][1][0];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) { rg0 = max(rg0, range[k][0][w]); rg1 = min(rg1, range[k][1][w]); }
+    rg0 = __builtin_amdgcn_readfirstlane(rg0);
+    rg1 = __builtin_amdgcn_readfirstlane(rg1);
+    n_tiles = rg0 >= 0 ? rg0 / NT + 1 : 0;
+    full = rg1 == 0x7fffffff ? 0 : rg1 / NT;
+  };
+
+  // The job: row tile qt, key tiles [t0, t1). A split tile runs as two
+  // pieces (piece 0: [0, h), piece 1: [h, n)) whose dQ partials
+  // dense_bwd_merge adds. Slot mode (a.q_pair == 0): slot k < n_qtiles takes
+  // row tile n_qtiles-1-k whole or its first half, slot n_qtiles+k its
+  // second half (tiles longer than q_split are halved). Pair mode: row
+  // tiles L = n-1-j and S = j form pair j; slot j takes L whole or its first
+  // piece, slot P+j takes S whole, slot 2P+odd+j L's second piece if L is
+  // split (only where that beats L whole, counting kQPieceCost tiles for the
+  // extra piece), an odd middle tile runs whole.
+  int qt, piece = 0, n_tiles, full, t0 = 0, t1;
+  bool split = false;
+  const int P = n_qtiles / 2, odd = n_qtiles & 1;
+  const bool middle = a.q_pair && odd && slot == 2 * P;
+  if (a.q_pair && !middle) {
+    const int j = slot < P ? slot : (slot < 2 * P ? slot - P : slot - 2 * P - odd);
+    const int L = n_qtiles - 1 - j;
+    int nL, fL, nS, fS;
+    tile_range(L, 0, nL, fL);
+    tile_range(j, 1, nS, fS);
+    const int h = min(nL, (nL + nS + kQPieceCost + 1) / 2);
+    const bool sp = h > 0 && h < nL && max(h, nL - h + nS + kQPieceCost) < nL;
+    if (slot < P) {
+      qt = L;
+      split = sp;
+      t1 = sp ? h : nL;
+    } else if (slot < 2 * P) {
+      qt = j;
+      t1 = nS;
+    } else {
+      if (!sp) return;  // whole workgroup: L ran whole
+      qt = L;
+      split = true;
+      piece = 1;
+      t0 = h;
+      t1 = nL;
+    }
+    n_tiles = qt == L ? nL : nS;
+    full = qt == L ? fL : fS;
+  } else {
+    piece = !middle && slot >= n_qtiles;
+    qt = middle ? P : n_qtiles - 1 - (piece ? slot - n_qtiles : slot);
+    tile_range(qt, 0, n_tiles, full);
+    split = !middle && n_tiles > a.q_split;
+    t0 = split && piece ? (n_tiles + 1) / 2 : 0;
+    t1 = split && !piece ? (n_tiles + 1) / 2 : n_tiles;
+    if (piece && !split) return;  // whole workgroup
+  }
   const int row = qt * 32 * WAVES + wave * 32 + col;
   const bool row_in = row < a.Q;
-  const int64_t H = a.H, D = a.D, N = a.N;
   const int64_t p = row_in ? a.pos[(int64_t)bi * a.Q + row] : -1;
 
   // remote keys [0, rlim), local keys [rlim, lhi]; bases of the exponents
@@ -210,22 +283,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     dl = a.delta[sidx];
     rho = a.rho[sidx];
   }
-  {
-    const int r0 = wave_max(lhi), r1 = wave_min(lhi >= 0 ? rlim : 0x7fffffff);
-    if (lane == 0) { range[0][wave] = r0; range[1][wave] = r1; }
-  }
-  __syncthreads();
-  int rg0 = range[0][0], rg1 = range[1][0];
-#pragma unroll
-  for (int w = 1; w < WAVES; ++w) { rg0 = max(rg0, range[0][w]); rg1 = min(rg1, range[1][w]); }
-  const int n_tiles = rg0 >= 0 ? rg0 / NT + 1 : 0;
-  // tiles below every valid row's remote limit: all keys remote, no masks
-  const int full = rg1 == 0x7fffffff ? 0 : rg1 / NT;
-  // a long item runs as two pieces: tiles [0, half) and [half, n_tiles)
-  const bool split = n_tiles > a.q_split;
-  const int t0 = split && piece ? (n_tiles + 1) / 2 : 0;
-  const int t1 = split && !piece ? (n_tiles + 1) / 2 : n_tiles;
-  if (piece && !split) return;  // whole workgroup
+  (void)n_tiles;
 
   const T* kg = reinterpret_cast<const T*>(a.k) + ((int64_t)bi * N * H + hh) * D;
   const T* vg = reinterpret_cast<const T*>(a.v) + ((int64_t)bi * N * H + hh) * D;
@@ -739,13 +797,30 @@ __global__ __launch_bounds__(256) void dense_bwd_merge_kernel(DenseArgs a, int n
   }
 }
 
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
 template <typename T, int DP>
-static hipError_t launch_fast(const DenseArgs& a, hipStream_t stream) {
+static hipError_t launch_fast(const DenseArgs& args, hipStream_t stream) {
+  DenseArgs a = args;
   const int n_rows = a.B * a.Qp;
   const int n_qtiles = (a.Q + 127) / 128;
   const int n_ktiles = (a.N + kKT - 1) / kKT;
   const int n_rtiles = a.Qp / kRT;
   const unsigned BH = (unsigned)(a.B * a.H);
+  // pair mode once slot mode's dQ slots outnumber the compute units
+  a.q_pair = 2 * (int64_t)n_qtiles * BH > device_cus();
+  const int q_slots = a.q_pair ? 3 * (n_qtiles / 2) + (n_qtiles & 1) : 2 * n_qtiles;
   const int n_lim = (n_rows + 255) / 256;
   const int64_t pairs = (int64_t)a.B * a.Q * a.H;
   const int n_pre = (int)((pairs + 256 / (DP / 8) - 1) / (256 / (DP / 8)));
@@ -754,7 +829,7 @@ static hipError_t launch_fast(const DenseArgs& a, hipStream_t stream) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   auto go = [&]<int LOGB>() {
-    hipLaunchKernelGGL((dense_bwd_dq_fast_kernel<T, DP, LOGB>), dim3(2 * n_qtiles * BH), dim3(256), 0, stream,
+    hipLaunchKernelGGL((dense_bwd_dq_fast_kernel<T, DP, LOGB>), dim3(q_slots * BH), dim3(256), 0, stream,
                        a, n_qtiles);
     if (hipPeekAtLastError() != hipSuccess) return;
     hipLaunchKernelGGL((dense_bwd_dkv_fast_kernel<T, DP, LOGB>), dim3(2 * n_ktiles * BH), dim3(256), 0,
