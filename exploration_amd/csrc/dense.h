@@ -37,6 +37,7 @@ struct DenseArgs {
   float* k_part;          // dK/dV partials, same order
   int q_split, k_split;   // items with more tiles than this run as two pieces
   int q_pair;             // dQ in pair mode (row tiles n-1-j and j share workgroups)
+  int k_pair;             // dK/dV in pair mode (key tiles j and n-1-j)
   // pipelined forward: a long row tile runs as two pieces whose partial
   // results dense_fwd_merge combines (fw0 null: never). Slot mode splits a
   // tile with more than f_split key tiles in halves; pair mode (f_pair) runs

@@ -41,6 +41,8 @@ constexpr int kKT = 128;       // keys per dK/dV workgroup and per dQ key tile
 // workgroup's dispatch, prologue and cold first tiles, the partial's store
 // and merge).
 constexpr int kQPieceCost = 6;
+// The same for a dK/dV key tile, in 64-row steps.
+constexpr int kKPieceCost = 4;
 constexpr int kRT = 64;        // query rows per dK/dV step / row-tile statistic
 constexpr int kMaxRTiles = 2048;
 constexpr size_t kMaxTable = size_t(4) << 30;
@@ -519,26 +521,74 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   __shared__ int list[kMaxRTiles];
   __shared__ int count;
 
+  __shared__ int pair_rows[2];
+
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 31, half = lane >> 5;
   const int BH = a.B * a.H;
-  const int bh = blockIdx.x % BH;
-  // all first pieces, then all second pieces; ascending key tiles (the
-  // first key tiles see the most rows)
-  const int kk = (int)(blockIdx.x / BH);
-  const int piece = kk >= n_ktiles;
-  const int kt_idx = piece ? kk - n_ktiles : kk;
+  const int bh = blockIdx.x % BH, slot = (int)(blockIdx.x / BH);
   const int bi = bh / a.H, hh = bh % a.H;
-  const int kb = kt_idx * kKT;
-  const int key = kb + 32 * wave + col;
   const int64_t H = a.H, D = a.D, N = a.N;
   const int64_t kstride = H * D;
+  const int* tmax = a.tmax + (int64_t)bi * n_rtiles;
+  const int* tmin = a.tmin + (int64_t)bi * n_rtiles;
+
+  // The job: key tile kt_idx, active row tiles [i0, i1) of its list. A
+  // split tile runs as two pieces whose dK/dV partials dense_bwd_merge adds.
+  // Slot mode (a.k_pair == 0): slot k < n_ktiles takes key tile k whole or
+  // its first half, slot n_ktiles+k its second half (tiles seen by more
+  // than k_split row tiles are halved; ascending key tiles, the first see
+  // the most rows). Pair mode: key tiles L = j and S = n-1-j form pair j;
+  // slot j takes L whole or its first piece, slot P+j takes S whole, slot
+  // 2P+odd+j L's second piece if L is split (only where that beats L whole,
+  // counting kKPieceCost row tiles for the extra piece); an odd middle tile
+  // runs whole.
+  int kt_idx, piece = 0, hsplit = 0;
+  bool split = false;
+  const int P = n_ktiles / 2, odd = n_ktiles & 1;
+  const bool middle = a.k_pair && odd && slot == 2 * P;
+  int pj = 0;
+  if (a.k_pair && !middle) {
+    pj = slot < P ? slot : (slot < 2 * P ? slot - P : slot - 2 * P - odd);
+    if (wave == 0) {
+      // row tiles reaching key tiles L and S
+#pragma unroll
+      for (int which = 0; which < 2; ++which) {
+        const int kb_w = (which ? n_ktiles - 1 - pj : pj) * kKT;
+        int n = 0;
+        for (int c0 = 0; c0 < n_rtiles; c0 += 64) {
+          const int t = c0 + lane;
+          n += __popcll(__ballot(t < n_rtiles && tmax[t] >= kb_w));
+        }
+        if (lane == 0) pair_rows[which] = n;
+      }
+    }
+    __syncthreads();
+    const int nL = pair_rows[0], nS = pair_rows[1];
+    const int h = min(nL, (nL + nS + kKPieceCost + 1) / 2);
+    const bool sp = h > 0 && h < nL && max(h, nL - h + nS + kKPieceCost) < nL;
+    if (slot < P) {
+      kt_idx = pj;
+      split = sp;
+    } else if (slot < 2 * P) {
+      kt_idx = n_ktiles - 1 - pj;
+    } else {
+      if (!sp) return;  // whole workgroup: L ran whole
+      kt_idx = pj;
+      split = true;
+      piece = 1;
+    }
+    hsplit = h;
+  } else {
+    piece = !middle && slot >= n_ktiles;
+    kt_idx = middle ? P : (piece ? slot - n_ktiles : slot);
+  }
+  const int kb = kt_idx * kKT;
+  const int key = kb + 32 * wave + col;
 
   // row tiles that see a key of this workgroup, in order; bit 0 marks tiles
   // whose rows all see every key of it (no masks)
   if (wave == 0) {
-    const int* tmax = a.tmax + (int64_t)bi * n_rtiles;
-    const int* tmin = a.tmin + (int64_t)bi * n_rtiles;
     int n = 0;
     for (int c0 = 0; c0 < n_rtiles; c0 += 64) {
       const int t = c0 + lane;
@@ -568,11 +618,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
   __syncthreads();
   const int n_act = count;
-  // a long item runs as two pieces: row tiles [0, half) and [half, n_act)
-  const bool split = n_act > a.k_split;
-  const int i0 = split && piece ? (n_act + 1) / 2 : 0;
-  const int i1 = split && !piece ? (n_act + 1) / 2 : n_act;
-  if (piece && !split) return;  // whole workgroup
+  if (!a.k_pair || middle) {
+    split = !middle && n_act > a.k_split;
+    hsplit = (n_act + 1) / 2;
+    if (piece && !split) return;  // whole workgroup
+  }
+  const int i0 = split && piece ? hsplit : 0;
+  const int i1 = split && !piece ? hsplit : n_act;
 
   const T* qg = reinterpret_cast<const T*>(a.q) + ((int64_t)bi * a.Q * H + hh) * D;
   const T* gg = reinterpret_cast<const T*>(a.dout) + ((int64_t)bi * a.Q * H + hh) * D;
@@ -821,6 +873,8 @@ static hipError_t launch_fast(const DenseArgs& args, hipStream_t stream) {
   // pair mode once slot mode's dQ slots outnumber the compute units
   a.q_pair = 2 * (int64_t)n_qtiles * BH > device_cus();
   const int q_slots = a.q_pair ? 3 * (n_qtiles / 2) + (n_qtiles & 1) : 2 * n_qtiles;
+  a.k_pair = 2 * (int64_t)n_ktiles * BH > device_cus();
+  const int k_slots = a.k_pair ? 3 * (n_ktiles / 2) + (n_ktiles & 1) : 2 * n_ktiles;
   const int n_lim = (n_rows + 255) / 256;
   const int64_t pairs = (int64_t)a.B * a.Q * a.H;
   const int n_pre = (int)((pairs + 256 / (DP / 8) - 1) / (256 / (DP / 8)));
@@ -832,7 +886,7 @@ static hipError_t launch_fast(const DenseArgs& args, hipStream_t stream) {
     hipLaunchKernelGGL((dense_bwd_dq_fast_kernel<T, DP, LOGB>), dim3(q_slots * BH), dim3(256), 0, stream,
                        a, n_qtiles);
     if (hipPeekAtLastError() != hipSuccess) return;
-    hipLaunchKernelGGL((dense_bwd_dkv_fast_kernel<T, DP, LOGB>), dim3(2 * n_ktiles * BH), dim3(256), 0,
+    hipLaunchKernelGGL((dense_bwd_dkv_fast_kernel<T, DP, LOGB>), dim3(k_slots * BH), dim3(256), 0,
                        stream, a, n_rtiles, n_ktiles);
     if (hipPeekAtLastError() != hipSuccess) return;
     hipLaunchKernelGGL((dense_bwd_merge_kernel<T, DP>), dim3((n_qtiles + n_ktiles) * BH, 2 * (DP / 32)),
