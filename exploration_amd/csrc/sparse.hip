@@ -320,8 +320,10 @@ __global__ __launch_bounds__(256, 2) void sparse_scan16_kernel(SparseArgs a) {
   constexpr int B = 1 << LOGB;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
-  const int h = blockIdx.y, bi = blockIdx.z;
-  const int64_t t0 = ((int64_t)blockIdx.x * 4 + wave) * KEYS;
+  // heads vary fastest across workgroups: the H head slices of a page are
+  // read by neighbouring workgroups at about the same time
+  const int h = (int)(blockIdx.x % (uint32_t)a.H), bi = blockIdx.z;
+  const int64_t t0 = ((int64_t)(blockIdx.x / (uint32_t)a.H) * 4 + wave) * KEYS;
   const int64_t n_tokens = a.kv.n_tokens;
   if (t0 >= n_tokens) return;
   const int64_t first_block = t0 >> LOGB;
@@ -604,6 +606,186 @@ __global__ __launch_bounds__(256) void sparse_select64_kernel(int64_t n_blocks, 
 }
 
 // ---------------------------------------------------------------------------
+// Radix top-k for k <= 64 and rows of at most NT*VMAX blocks: the row's
+// 64-bit keys (ordered score bits, ~block id: all distinct) stay in
+// registers; the bytes shared by every key (the row's min and max key agree
+// on them) are skipped, then one byte per pass: a 256-bin LDS histogram of
+// the keys that still match the prefix, a suffix scan, and the bin that
+// holds the k-th largest key. The pass ends early when that bin's keys are
+// all selected. The selected keys are compacted and rank-sorted.
+template <int NT, int VMAX>
+__global__ __launch_bounds__(NT) void sparse_select_radix_kernel(int64_t n_blocks, int topk, int64_t id_base,
+                                                                 const float* scores, int64_t* ids, float* top,
+                                                                 float* log_zr) {
+  constexpr int NW = NT / 64;
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t wsum[4];
+  __shared__ uint64_t sel[64];
+  __shared__ uint64_t red_k[2][NW];
+  __shared__ float red_m[NW], red_s[NW];
+  __shared__ uint32_t ctrl[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row = blockIdx.x;
+  const float* s = scores + row * n_blocks;
+  const int n = (int)n_blocks;
+  if (tid == 0) ctrl[3] = 0;
+  uint64_t key[VMAX];
+  float m = kNegInf, sum = 0.f;
+  uint64_t kmax = 0, kmin = ~0ull;
+  // unconditional loads (clamped index): all VMAX in flight together
+  float xs[VMAX];
+#pragma unroll
+  for (int v = 0; v < VMAX; ++v) xs[v] = s[tid + NT * v < n ? tid + NT * v : n - 1];
+#pragma unroll
+  for (int v = 0; v < VMAX; ++v) {
+    const int i = tid + NT * v;
+    const float x = i < n ? xs[v] : kNegInf;
+    key[v] = ((uint64_t)ordered_bits(x) << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+    if (i < n) {
+      kmax = key[v] > kmax ? key[v] : kmax;
+      kmin = key[v] < kmin ? key[v] : kmin;
+    }
+    if (x > m) {
+      sum = (m == kNegInf ? 0.f : sum * __expf(m - x)) + 1.f;
+      m = x;
+    } else if (x != kNegInf) {
+      sum += __expf(x - m);
+    }
+  }
+  // row logsumexp and the key range
+  float mw = m;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mw = fmaxf(mw, __shfl_xor(mw, off, 64));
+  float sw = (m == kNegInf) ? 0.f : sum * __expf(m - mw);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    sw += __shfl_xor(sw, off, 64);
+    const uint64_t a = shfl_xor64(kmax, off), b = shfl_xor64(kmin, off);
+    kmax = a > kmax ? a : kmax;
+    kmin = b < kmin ? b : kmin;
+  }
+  if (lane == 0) {
+    red_m[wave] = mw;
+    red_s[wave] = sw;
+    red_k[0][wave] = kmax;
+    red_k[1][wave] = kmin;
+  }
+  __syncthreads();
+  kmax = red_k[0][0];
+  kmin = red_k[1][0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) {
+    kmax = red_k[0][w] > kmax ? red_k[0][w] : kmax;
+    kmin = red_k[1][w] < kmin ? red_k[1][w] : kmin;
+  }
+  if (tid == 0) {
+    float mm = red_m[0];
+    for (int w = 1; w < NW; ++w) mm = fmaxf(mm, red_m[w]);
+    float tot = 0.f;
+    if (mm != kNegInf)
+      for (int w = 0; w < NW; ++w) tot += red_m[w] == kNegInf ? 0.f : red_s[w] * __expf(red_m[w] - mm);
+    log_zr[row] = (mm == kNegInf || !(tot > 0.f)) ? kNegInf : mm + __logf(tot);
+  }
+  // select: keys whose top (64 - shift) bits are >= prefix
+  int shift = 64;
+  uint64_t prefix = 0;
+  if (n > topk) {
+    const uint64_t diff = kmax ^ kmin;  // nonzero: n >= 2 distinct keys
+    const int common = __builtin_clzll(diff) & ~7;
+    shift = 64 - common;
+    prefix = common ? (kmax >> shift) : 0;
+    uint32_t kk = (uint32_t)topk;
+    while (true) {
+      shift -= 8;
+      if (tid < 256) hist[tid] = 0;
+      __syncthreads();
+      // Scores crowd into few bins (often one), and same-address LDS atomics
+      // serialise: the lanes sharing the first two leaders' digits add their
+      // count with one atomic each, the rest add one by one.
+#pragma unroll
+      for (int v = 0; v < VMAX; ++v) {
+        bool match = tid + NT * v < n && (shift + 8 == 64 || (key[v] >> (shift + 8)) == prefix);
+        const uint32_t digit = (uint32_t)(key[v] >> shift) & 255u;
+#pragma unroll
+        for (int round = 0; round < 2; ++round) {
+          const uint64_t act = __ballot(match);
+          if (act == 0) break;
+          const int leader = __builtin_ctzll(act);
+          const uint32_t ld = (uint32_t)__builtin_amdgcn_readlane((int)digit, leader);
+          const bool same = match && digit == ld;
+          const uint64_t group = __ballot(same);
+          if (lane == leader) atomicAdd(&hist[ld], (uint32_t)__popcll(group));
+          match = match && !same;
+        }
+        if (match) atomicAdd(&hist[digit], 1u);
+      }
+      __syncthreads();
+      // suffix sums: thread t < 256 holds bin 255 - t
+      uint32_t hv = 0, incl = 0;
+      if (tid < 256) {
+        hv = hist[255 - tid];
+        incl = hv;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const uint32_t y = __shfl_up(incl, off, 64);
+          if (lane >= off) incl += y;
+        }
+        if (lane == 63) wsum[wave] = incl;
+      }
+      __syncthreads();
+      if (tid < 256) {
+        for (int w = 0; w < wave; ++w) incl += wsum[w];
+        const uint32_t above = incl - hv;
+        if (above < kk && incl >= kk) {
+          ctrl[0] = 255u - (uint32_t)tid;
+          ctrl[1] = kk - above;
+          ctrl[2] = hv;
+        }
+      }
+      __syncthreads();
+      const uint32_t d = ctrl[0], hd = ctrl[2];
+      kk = ctrl[1];
+      prefix = (prefix << 8) | d;
+      if (hd == kk || shift == 0) break;
+    }
+  }
+  // compaction: slots within the wave from ballots, one atomic per wave
+  uint32_t slot[VMAX];
+  uint32_t wave_cnt = 0;
+  const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+  for (int v = 0; v < VMAX; ++v) {
+    const bool take = tid + NT * v < n && (shift == 64 || (key[v] >> shift) >= prefix);
+    const uint64_t mask = __ballot(take);
+    slot[v] = take ? wave_cnt + (uint32_t)__popcll(mask & below) : ~0u;
+    wave_cnt += (uint32_t)__popcll(mask);
+  }
+  if (wave_cnt) {
+    uint32_t base = 0;
+    if (lane == 0) base = atomicAdd(&ctrl[3], wave_cnt);
+    base = (uint32_t)__builtin_amdgcn_readlane((int)base, 0);
+#pragma unroll
+    for (int v = 0; v < VMAX; ++v)
+      if (slot[v] != ~0u) sel[base + slot[v]] = key[v];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  const int cnt = (int)ctrl[3];
+  if (lane < cnt) {
+    const uint64_t mine = sel[lane];
+    int rank = 0;
+    for (int j = 0; j < cnt; ++j) rank += sel[j] > mine;
+    const uint32_t ob = (uint32_t)(mine >> 32);
+    const float sc = __uint_as_float((ob & 0x80000000u) ? (ob & 0x7fffffffu) : ~ob);
+    top[row * topk + rank] = sc;
+    ids[row * topk + rank] = sc != kNegInf ? (int64_t)(0xffffffffu - (uint32_t)(mine & 0xffffffffu)) + id_base : -1;
+  } else if (lane < topk) {
+    top[row * topk + lane] = kNegInf;
+    ids[row * topk + lane] = -1;
+  }
+}
+
+// ---------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t ordered_bits(float x) {
   const uint32_t u = __float_as_uint(x);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
@@ -851,28 +1033,56 @@ __global__ __launch_bounds__(256) void sparse_pop_kernel(SparseArgs a) {
   }
 }
 
+// One wave per row. The slot partials were written just before, so the
+// kernel is bound by load latency: each lane fetches one chunk's (max, mass)
+// and the chunk outputs are read eight chunks at a time, all loads of a
+// round in flight together.
 template <typename T, int DP>
 __global__ __launch_bounds__(64) void sparse_merge_kernel(SparseArgs a, int chunks) {
+  constexpr int S = DP + 2;
+  constexpr int NJ = DP / 64;
+  constexpr int R = 8;
   const int64_t row = blockIdx.x;
   const int lane = threadIdx.x;
-  const float* src = a.partial + row * chunks * (DP + 2);
+  const float* src = a.partial + row * chunks * S;
   float mm = kNegInf;
-  for (int c = 0; c < chunks; ++c) mm = fmaxf(mm, src[c * (DP + 2)]);
+  for (int c = lane; c < chunks; c += 64) mm = fmaxf(mm, src[(int64_t)c * S]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mm = fmaxf(mm, __shfl_xor(mm, off, 64));
   float l = 0.f;
-  float o[DP / 64];
+  float o[NJ];
 #pragma unroll
-  for (int j = 0; j < DP / 64; ++j) o[j] = 0.f;
-  for (int c = 0; c < chunks; ++c) {
-    const float* pc = src + c * (DP + 2);
-    const float w = mm == kNegInf ? 0.f : fast_exp2(pc[0] - mm);
-    l += w * pc[1];
+  for (int j = 0; j < NJ; ++j) o[j] = 0.f;
+  for (int c0 = 0; c0 < chunks; c0 += 64) {
+    const int c = c0 + lane;
+    float w = 0.f;
+    if (c < chunks && mm != kNegInf) {
+      const float* pc = src + (int64_t)c * S;
+      w = fast_exp2(pc[0] - mm);
+      l += w * pc[1];
+    }
+    const int n = chunks - c0 < 64 ? chunks - c0 : 64;
+    for (int i0 = 0; i0 < n; i0 += R) {
+      float v[R][NJ];
 #pragma unroll
-    for (int j = 0; j < DP / 64; ++j) o[j] += w * pc[2 + lane + 64 * j];
+      for (int i = 0; i < R; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+          v[i][j] = i0 + i < n ? src[(int64_t)(c0 + i0 + i) * S + 2 + lane + 64 * j] : 0.f;
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        const float wi = __shfl(w, i0 + i, 64);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) o[j] += wi * v[i][j];
+      }
+    }
   }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off, 64);
   const float inv = l > 0.f ? 1.f / l : 0.f;
   T* out = reinterpret_cast<T*>(a.out) + row * a.D;
 #pragma unroll
-  for (int j = 0; j < DP / 64; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     const int d = lane + 64 * j;
     if (d < a.D) out[d] = from_float<T>(o[j] * inv);
   }
@@ -886,6 +1096,8 @@ static hipError_t scores_dp(const SparseArgs& a, hipStream_t s) {
   dim3 grid((unsigned)((chunks + 3) / 4), a.H, a.B);
   if constexpr (sizeof(T) == 2 && DP <= 128) {
     if (a.D % 32 == 0) {
+      if ((chunks + 3) / 4 * a.H >= (int64_t(1) << 31)) return hipErrorInvalidConfiguration;
+      grid = dim3((unsigned)((chunks + 3) / 4 * a.H), 1, a.B);
       auto go16 = [&]<int LOGB>() {
         if (a.kv.page_table) hipLaunchKernelGGL((sparse_scan16_kernel<T, DP, true, LOGB>), grid, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((sparse_scan16_kernel<T, DP, false, LOGB>), grid, dim3(256), 0, s, a);
@@ -940,7 +1152,13 @@ hipError_t launch_sparse_scores(int dtype, const SparseArgs& a, hipStream_t stre
 hipError_t launch_sparse_select(int64_t rows, int64_t n_blocks, int topk, int64_t id_base,
                                 const float* scores, int64_t* ids, float* top, float* log_zr,
                                 hipStream_t stream) {
-  if (topk <= 64)
+  if (topk <= 64 && n_blocks <= 512 * 16)
+    hipLaunchKernelGGL((sparse_select_radix_kernel<512, 16>), dim3((unsigned)rows), dim3(512), 0, stream, n_blocks,
+                       topk, id_base, scores, ids, top, log_zr);
+  else if (topk <= 64 && n_blocks <= 512 * 32)
+    hipLaunchKernelGGL((sparse_select_radix_kernel<512, 32>), dim3((unsigned)rows), dim3(512), 0, stream, n_blocks,
+                       topk, id_base, scores, ids, top, log_zr);
+  else if (topk <= 64)
     hipLaunchKernelGGL(sparse_select64_kernel, dim3((unsigned)rows), dim3(256), 0, stream, n_blocks, topk, id_base,
                        scores, ids, top, log_zr);
   else

@@ -108,6 +108,29 @@ def test_select_exact_ties_and_short_rows(device):
     assert ids.tolist() == [[1000, 1002, 1003, 1005, 1007, 1008, 1009, 1004]]
 
 
+@pytest.mark.parametrize("n", [1, 40, 64, 65, 4097, 8192, 8193, 16384, 16385])
+def test_select_row_lengths(device, n):
+    """Every selection kernel size class (up to 8192 and 16384 blocks per
+    row in registers, longer rows streamed), rows shorter than topk, exact
+    ties at the cut, all -inf rows, and continuous scores."""
+    print(f"sparse select n={n}", flush=True)
+    g = torch.Generator().manual_seed(n)
+    rows = 6
+    s = torch.randn(rows, n, generator=g) * 3
+    s[1] = torch.randint(0, 6, (n,), generator=g).float()  # ties straddle every cut
+    s[2] = 2.5
+    s[3] = -math.inf
+    s[4, ::3] = -math.inf
+    s[5] = torch.randint(-3, 3, (n,), generator=g).float() * 1e30
+    for topk in (1, 17, 64):
+        values, ids, zr = select_blocks(s.to(device), topk, id_base=7)
+        ev, ei, ez = osp.select_topk(s, topk)
+        ei = torch.where(ei >= 0, ei + 7, ei)
+        assert torch.equal(ids.cpu(), ei), (n, topk)
+        assert torch.equal(values.cpu(), ev), (n, topk)
+        assert_close(zr, ez, torch.float32, "log_zr")
+
+
 def test_pop_with_given_selection(device):
     """sparse_pop on a caller-supplied selection (including -1 slots)."""
     print("sparse pop", flush=True)
