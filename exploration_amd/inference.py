@@ -10,10 +10,15 @@ global read rounds through the sparse top-k operator with no host
 synchronisation.
 
 Cache tiers: ``"cuda"`` keeps K/V in HBM (the cfg5 decode: 131,072 tokens x
-16 heads x 64 dims is 512 MiB). ``"cpu"`` keeps them in host memory and the
-operator streams pages through a device staging pool (``sparse.HostPages``).
-The reference's disk tier and multi-rank sharding are not built.
+16 heads x 64 dims is 512 MiB). ``"cpu"`` keeps them in pinned host memory
+and ``"disk"`` in a file-backed mapping under ``cache_dir`` (contexts larger
+than host memory); for both the operator streams K through device buffers
+and gathers the touched blocks into a device pool (``sparse.HostPages``).
+Multi-rank sharding is not built (one GPU).
 """
+import os
+import shutil
+import tempfile
 from dataclasses import asdict, dataclass
 
 import torch
@@ -62,8 +67,6 @@ def plan_inference(model, batch, length, *, cache="auto", memory_fraction=.8, pa
         raise ValueError("positive sizes and 0 < memory_fraction < 1 required")
     if cache not in ("auto", "cuda", "cpu", "disk"):
         raise ValueError("cache must be auto/cuda/cpu/disk")
-    if cache == "disk":
-        raise NotImplementedError("the disk KV tier is not built; use cuda or cpu")
     param = next(model.parameters())
     b, dim, heads = model.block_size, model.dim, model.heads
     element = param.element_size()
@@ -79,12 +82,22 @@ def plan_inference(model, batch, length, *, cache="auto", memory_fraction=.8, pa
             cache = "cuda"
         elif host is None or total + 4 * workspace < host * .7:
             cache = "cpu"
+        elif cache_dir:
+            cache = "disk"
         else:
-            raise MemoryError(f"KV requires {total / GiB:.2f} GiB; neither HBM nor host memory holds it")
+            raise MemoryError(f"KV requires {total / GiB:.2f} GiB; neither HBM nor host memory holds it "
+                              "(give cache_dir for the disk tier)")
     if cache == "cuda" and (not param.is_cuda or total + 4 * workspace >= budget):
-        raise MemoryError(f"GPU KV requires {total / GiB:.2f} GiB plus workspace; select cache=auto/cpu")
+        raise MemoryError(f"GPU KV requires {total / GiB:.2f} GiB plus workspace; select cache=auto/cpu/disk")
     if cache == "cpu" and host is not None and total + 4 * workspace > host * .7:
-        raise MemoryError(f"CPU KV requires {total / GiB:.2f} GiB; available RAM {host / GiB:.2f} GiB")
+        raise MemoryError(f"CPU KV requires {total / GiB:.2f} GiB; available RAM {host / GiB:.2f} GiB; "
+                          "select the disk tier")
+    if cache == "disk":
+        if not cache_dir:
+            raise ValueError("the disk KV tier needs cache_dir on a filesystem with room for the cache")
+        os.makedirs(cache_dir, exist_ok=True)
+        if total + GiB > shutil.disk_usage(cache_dir).free:
+            raise MemoryError(f"disk KV requires {total / GiB:.2f} GiB; not free under {cache_dir}")
     page = max(b, min(page_tokens, workspace // max(2 * batch * dim * element, 1)) // b * b)
     enc = max(b, min(encoder_chunk, workspace // max(24 * batch * dim * element, 1)) // b * b)
     qc = max(1, min(query_chunk, workspace // max(batch * heads * model.topk * b * 4, 1)))
@@ -94,36 +107,68 @@ def plan_inference(model, batch, length, *, cache="auto", memory_fraction=.8, pa
 
 
 class KVCache(TensorPages):
-    """Write-once raw K/V ``[B,N,H,hd]`` in HBM (``"cuda"``) or pinned host
-    memory (``"cpu"``), read through the page protocol
-    (``st/runtime/inference.py:19-62``)."""
+    """Write-once raw K/V ``[B,N,H,hd]`` in HBM (``"cuda"``), pinned host
+    memory (``"cpu"``) or a file-backed mapping (``"disk"``), read through the
+    page protocol (``st/runtime/inference.py:19-62``). The disk tier's file
+    lives in a private temporary directory under ``cache_dir`` with its
+    blocks allocated up front (a full filesystem fails here, not half-way
+    through a prefill); ``close`` removes it."""
 
-    def __init__(self, batch, length, heads, dim, dtype, device, plan, offset=0):
+    def __init__(self, batch, length, heads, dim, dtype, device, plan, offset=0, cache_dir=None):
         shape = (batch, length, heads, dim)
+        self.directory = None
         if plan.cache == "cuda":
             k, v = (torch.empty(shape, dtype=dtype, device=device) for _ in range(2))
-        else:
+        elif plan.cache == "cpu":
             k, v = (torch.empty(shape, dtype=dtype, pin_memory=True) for _ in range(2))
+        elif plan.cache == "disk":
+            k, v = self._map_file(shape, dtype, cache_dir)
+        else:
+            raise ValueError(f"unknown cache tier {plan.cache!r}")
         super().__init__(k, v, plan.page_tokens, offset)
         self.tier = plan.cache
         self.device = torch.device(device)
+
+    def _map_file(self, shape, dtype, cache_dir):
+        """K and V as the two halves of one shared file mapping."""
+        self.directory = tempfile.mkdtemp(prefix="st-kv-", dir=cache_dir)
+        count = shape[0] * shape[1] * shape[2] * shape[3]
+        nbytes = 2 * count * torch.empty((), dtype=dtype).element_size()
+        path = os.path.join(self.directory, "kv.bin")
+        try:
+            with open(path, "xb") as f:
+                if hasattr(os, "posix_fallocate"):
+                    os.posix_fallocate(f.fileno(), 0, nbytes)
+                else:
+                    f.truncate(nbytes)
+            flat = torch.from_file(path, shared=True, size=2 * count, dtype=dtype)
+        except BaseException:
+            shutil.rmtree(self.directory, ignore_errors=True)
+            self.directory = None
+            raise
+        return flat[:count].view(shape), flat[count:].view(shape)
 
     def write(self, start, k, v):
         lo = start - self.offset
         if lo < 0 or lo + k.shape[1] > self.length:
             raise ValueError("KV write outside owned shard")
-        self.k[:, lo:lo + k.shape[1]].copy_(k, non_blocking=True)
-        self.v[:, lo:lo + v.shape[1]].copy_(v, non_blocking=True)
+        # pageable file memory: a synchronous copy; HBM and pinned: stream-ordered
+        asynchronous = self.tier != "disk"
+        self.k[:, lo:lo + k.shape[1]].copy_(k, non_blocking=asynchronous)
+        self.v[:, lo:lo + v.shape[1]].copy_(v, non_blocking=asynchronous)
 
     def reader(self, score_tokens):
         """What the sparse operator reads: the cache itself in HBM, or a
-        streaming view of the host tier."""
+        streaming view of the host or disk tier."""
         if self.tier == "cuda":
             return self
         return HostPages(self.k, self.v, self.device, chunk_tokens=score_tokens, offset=self.offset)
 
     def close(self):
         self.k, self.v = None, None
+        if self.directory is not None:
+            shutil.rmtree(self.directory, ignore_errors=True)
+            self.directory = None
 
     def __enter__(self):
         return self
@@ -170,7 +215,8 @@ class InferenceSession:
         if positions.numel() * m.dim * self.dtype.itemsize > self.max_query_bytes:
             raise MemoryError("query states exceed max_query_states_mb; evaluate fewer positions")
         self.plan = plan_inference(m, batch, n, **self.options)
-        self.cache = KVCache(batch, n, m.heads, m.hd, self.dtype, self.device, self.plan)
+        self.cache = KVCache(batch, n, m.heads, m.hd, self.dtype, self.device, self.plan,
+                             cache_dir=self.options["cache_dir"])
         self.positions = positions
         self.query_states = torch.zeros(batch, positions.shape[1], m.dim, dtype=self.dtype, device=self.device)
         dev_pos = positions.to(self.device)

@@ -150,7 +150,9 @@ class PagedKV:
 class HostPages:
     """Host-resident raw K/V ``[B, N, H, D]`` (absolute tokens
     ``[offset, offset + N)``) streamed to ``device`` in chunks of
-    ``chunk_tokens`` tokens. Pinned tensors make the copies asynchronous."""
+    ``chunk_tokens`` tokens. Pinned tensors are copied to the device
+    directly; pageable ones (a file mapping) are first copied into pinned
+    staging buffers, so the device copies stay asynchronous."""
 
     def __init__(self, k, v, device, chunk_tokens=65536, offset=0):
         if k.shape != v.shape or k.ndim != 4 or k.device.type != "cpu":
@@ -173,16 +175,25 @@ def _sparse_host(q, cache, positions, b, topk, return_selection):
     main = torch.cuda.current_stream(q.device)
     copier = torch.cuda.Stream(q.device)
     copier.wait_stream(main)  # device->host writes of the cache issued on the main stream come first
-    bufs = [torch.empty(batch * min(chunk, n) * heads * dim, device=q.device, dtype=q.dtype) for _ in range(2)]
+    size = batch * min(chunk, n) * heads * dim
+    bufs = [torch.empty(size, device=q.device, dtype=q.dtype) for _ in range(2)]
+    # pageable source: the CPU fills pinned buffer i%2 with chunk i while the
+    # device still copies and scores chunk i-1
+    stage = None if cache.k.is_pinned() else [torch.empty(size, dtype=q.dtype, pin_memory=True) for _ in range(2)]
     ready = [torch.cuda.Event() for _ in range(2)]
     free = [torch.cuda.Event() for _ in range(2)]
     for i, lo in enumerate(range(0, n, chunk)):
         hi, slot = min(n, lo + chunk), i % 2
         part = bufs[slot][:batch * (hi - lo) * heads * dim].view(batch, hi - lo, heads, dim)
+        src = cache.k[:, lo:hi]
+        if stage is not None:
+            if i >= 2:
+                ready[slot].synchronize()  # the device copy out of this buffer (chunk i-2) is done
+            src = stage[slot][:part.numel()].view(part.shape).copy_(src)
         with torch.cuda.stream(copier):
             if i >= 2:
                 copier.wait_event(free[slot])
-            part.copy_(cache.k[:, lo:hi], non_blocking=True)
+            part.copy_(src, non_blocking=True)
             ready[slot].record(copier)
         main.wait_event(ready[slot])
         g0, g1 = lo // b, -(-hi // b)
@@ -196,11 +207,12 @@ def _sparse_host(q, cache, positions, b, topk, return_selection):
     wanted = torch.cat((ids, local), -1).reshape(batch, -1) - off // b
     wanted = wanted.cpu()
     table = torch.zeros((batch, n_blocks), dtype=torch.int32)
-    rows, blocks = [], []
+    rows, blocks, placed = [], [], 0
     for r in range(batch):
         w = wanted[r]
         uniq = w[(w >= 0) & (w < n_blocks)].unique()
-        table[r, uniq] = torch.arange(len(blocks), len(blocks) + len(uniq), dtype=torch.int32)
+        table[r, uniq] = torch.arange(placed, placed + len(uniq), dtype=torch.int32)
+        placed += len(uniq)
         rows.append(torch.full_like(uniq, r))
         blocks.append(uniq)
     rows, blocks = torch.cat(rows), torch.cat(blocks)

@@ -9,7 +9,8 @@
   hidden states and K/V as model.encode): logits equal model.forward's
   sparse path;
 * the host tier (K/V in pinned host memory, streamed scan and paged read)
-  equals the HBM tier.
+  and the disk tier (a file mapping, staged through pinned buffers) equal
+  the HBM tier, and the disk tier leaves its directory empty.
 fp32 models; tolerance 1e-4 relative to the largest logit.
 """
 import pytest
@@ -69,13 +70,17 @@ def test_sparse_session_equals_model_forward(device):
     close(got, want)
 
 
+@pytest.mark.parametrize("tier", ["cpu", "disk"])
 @pytest.mark.parametrize("topk", [4, 64])
-def test_host_tier_equals_hbm_tier(device, topk):
-    print(f"session host tier topk={topk}", flush=True)
+def test_host_tier_equals_hbm_tier(device, topk, tier, tmp_path):
+    print(f"session {tier} tier topk={topk}", flush=True)
     n = 1024
     m = model(device, topk=topk)
-    ids, _ = synthetic_lm_batch(64, n, batch=1, seed=5)
-    positions = torch.tensor([[n - 1, 600, 17, n - 300]])
-    hbm = session_logits(m, ids, positions, cache="cuda", encoder_chunk=4096)
-    host = session_logits(m, ids, positions, cache="cpu", encoder_chunk=4096, page_tokens=256)
+    ids, _ = synthetic_lm_batch(64, n, batch=2, seed=5)
+    positions = torch.tensor([[n - 1, 600, 17, n - 300], [n - 2, 33, 511, 512]])
+    # same encoder chunking in both sessions: identical hidden states and K/V
+    hbm = session_logits(m, ids, positions, cache="cuda", encoder_chunk=256)
+    host = session_logits(m, ids, positions, cache=tier, cache_dir=str(tmp_path), encoder_chunk=256,
+                          page_tokens=240)
     close(host, hbm)
+    assert list(tmp_path.iterdir()) == []
