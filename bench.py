@@ -141,30 +141,39 @@ def bench_model(args, torch, device):
     """cfg5: one training step of a stack_100m-shaped model (random init, bf16
     autocast, AdamW, checkpointed chunks) on uniform token ids, batch 1,
     length 8192, every position supervised; tokens/s over the timed steps
-    (the reference engine's figure, st/runtime/engine.py:192)."""
+    (the reference engine's figure, st/runtime/engine.py:192). The step runs
+    eagerly first, then captured into one HIP graph and replayed
+    (``GraphedStep``); ``tokens_per_s`` is the graphed figure."""
     from exploration_amd.model import STACK_100M, build_model
-    from exploration_amd.train import check_step, make_optimizer, synthetic_lm_batch, train_step
+    from exploration_amd.train import GraphedStep, check_step, make_optimizer, synthetic_lm_batch, train_step
 
     length = 8192
     model = build_model(STACK_100M, execution={"checkpoint_chunks": True}, device=device)
-    opt = make_optimizer(model)
+    opt = make_optimizer(model, capturable=True)
     ids, targets = synthetic_lm_batch(STACK_100M["vocab_size"], length, batch=1, seed=0, device=device)
     losses = []
 
-    def step():
-        losses.append(train_step(model, opt, ids, targets)[0])
+    def eager():
+        losses.append(train_step(model, opt, ids, targets, width=length)[0])
 
-    per, wall = timed_steps(step, 3, args.model_steps, torch)
-    loss, _, count = train_step(model, opt, ids, targets)
+    per_e, wall_e = timed_steps(eager, 3, args.model_steps, torch)
+    graphed = GraphedStep(model, opt, ids, targets, warmup=1)
+
+    def replay():
+        losses.append(graphed(ids, targets)[0].clone())
+
+    per, wall = timed_steps(replay, 2, args.model_steps, torch)
+    loss, _, count = graphed(ids, targets)
     check_step(loss, count)
-    ms = sum(per) / len(per)
+    ms, ms_e = sum(per) / len(per), sum(per_e) / len(per_e)
     chunk = model._chunk_size(length)
     result = {"tokens_per_s": length / (ms * 1e-3), "ms_mean": ms, "ms_median": statistics.median(per),
-              "wall_s": wall, "steps": args.model_steps, "warmup": 3,
+              "wall_s": wall, "steps": args.model_steps, "warmup": 3, "graphed": True,
+              "eager_tokens_per_s": length / (ms_e * 1e-3), "eager_ms_mean": ms_e,
               "params": sum(p.numel() for p in model.parameters()),
               "dense_calls_per_step": -(-(length - 1) // chunk), "query_chunk": chunk,
               "loss_first": float(losses[0]), "loss_last": float(loss)}
-    del opt
+    del opt, graphed
     result["decode"] = bench_decode(model, torch)
     return result
 

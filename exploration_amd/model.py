@@ -334,9 +334,14 @@ class StackModel(nn.Module):
         ctx = ctx.reshape(*z.shape[:2], self.dim)
         return checkpoint(finish, z, ctx, use_reentrant=False, preserve_rng_state=False) if ckpt else finish(z, ctx)
 
-    def forward_loss(self, input_ids, targets, sup=None, offset=0):
+    def forward_loss(self, input_ids, targets, sup=None, offset=0, width=None):
         """Dense training loss (``stack.py:215-279``): SUM of token losses and
-        counts at the supervised positions, never ``[B,N,V]``."""
+        counts at the supervised positions, never ``[B,N,V]``.
+
+        ``width`` (optional) is the number of query slots per row; it must be
+        at least the largest supervised count of a row (``N`` always is).
+        Given, it spares the one host synchronisation that reads that count,
+        so the step can be captured into a graph."""
         if input_ids.ndim != 2 or input_ids.shape != targets.shape or min(input_ids.shape) < 1:
             raise ValueError("ids and targets must have identical nonempty [B,N] shape")
         if sup is None:
@@ -345,8 +350,11 @@ class StackModel(nn.Module):
             raise ValueError("sup must be bool [B,N]")
         sup = sup & (targets != -100)
         batch, n = input_ids.shape
-        width = int(sup.sum(1).max())
-        width = max(width, 1)
+        if width is None:
+            width = int(sup.sum(1).max())
+        elif not 1 <= width <= n:
+            raise ValueError("width must lie in [1, sequence length]")
+        width = max(int(width), 1)
         order = torch.arange(n, device=input_ids.device)[None].expand(batch, -1)
         order = torch.where(sup, order, n).sort(1).values[:, :width]
         valid = order < n

@@ -4,30 +4,78 @@ the supervised tokens divided by their count, gradient clipping, AdamW with
 the reference's betas (0.9, 0.95) and defaults (lr 3e-4, weight decay 0.01,
 clip 1.0; ``engine.py:88-119``, ``cli.py:71-73``).
 
-Unlike the reference, a step makes no host synchronisation: the reference's
-checks that the batch has supervised tokens and that the loss is finite
-(``engine.py:170-175``) read device values back every step; here they are
-left to the caller (``check_step``).
+The reference's checks that the batch has supervised tokens and that the
+loss is finite (``engine.py:170-175``) read device values back every step;
+here they are left to the caller (``check_step``). With ``width`` given, a
+step makes no host synchronisation at all, and ``GraphedStep`` captures the
+whole step (forward, backward, clipping, optimizer) into one HIP graph: the
+model's ~20,000 small kernels per step then cost one graph launch instead
+of as many launches from Python.
 """
 import torch
 
 
-def make_optimizer(model, lr=3e-4, weight_decay=0.01):
+def make_optimizer(model, lr=3e-4, weight_decay=0.01, capturable=False):
     fused = next(model.parameters()).is_cuda
-    return torch.optim.AdamW(model.parameters(), lr=lr, betas=(0.9, 0.95), weight_decay=weight_decay, fused=fused)
+    return torch.optim.AdamW(model.parameters(), lr=lr, betas=(0.9, 0.95), weight_decay=weight_decay, fused=fused,
+                             capturable=capturable and fused)
 
 
-def train_step(model, optimizer, ids, targets, sup=None, clip_grad=1.0, precision="bf16"):
+def train_step(model, optimizer, ids, targets, sup=None, clip_grad=1.0, precision="bf16", width=None,
+               autocast_cache=True):
     """Forward loss, backward, clip, optimizer step. Returns device tensors
     (mean loss, gradient norm, supervised count)."""
     optimizer.zero_grad(set_to_none=True)
-    with torch.autocast(ids.device.type, dtype=torch.bfloat16, enabled=precision == "bf16"):
-        result = model.forward_loss(ids, targets, sup)
+    with torch.autocast(ids.device.type, dtype=torch.bfloat16, enabled=precision == "bf16",
+                        cache_enabled=autocast_cache):
+        result = model.forward_loss(ids, targets, sup, width=width)
         loss = result["loss_sum"] / result["count"]
     loss.backward()
     norm = torch.nn.utils.clip_grad_norm_(model.parameters(), clip_grad)
     optimizer.step()
     return loss.detach(), norm.detach(), result["count"]
+
+
+class GraphedStep:
+    """``train_step`` captured once into a HIP graph and replayed.
+
+    ``ids``/``targets`` fix the batch shape; each call copies the new batch
+    into the captured input buffers and replays the graph. Every position
+    may be supervised (the captured width is the sequence length), so any
+    targets of that shape are valid. The optimizer must be capturable
+    (``make_optimizer(model, capturable=True)``). Construction runs
+    ``warmup`` eager steps on a side stream first (they update the model
+    like any step), then captures one step without running it. Returns the
+    same device tensors as ``train_step``; they are overwritten by the next
+    call."""
+
+    def __init__(self, model, optimizer, ids, targets, clip_grad=1.0, precision="bf16", warmup=3):
+        if not ids.is_cuda:
+            raise ValueError("graph capture needs the model and batch on the GPU")
+        if not all(g.get("capturable", False) for g in optimizer.param_groups):
+            raise ValueError("the optimizer must be built with capturable=True")
+        self.ids, self.targets = ids.clone(), targets.clone()
+        options = dict(clip_grad=clip_grad, precision=precision, width=ids.shape[1], autocast_cache=False)
+
+        def step():
+            return train_step(model, optimizer, self.ids, self.targets, **options)
+
+        main = torch.cuda.current_stream(ids.device)
+        side = torch.cuda.Stream(ids.device)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            for _ in range(max(1, warmup)):
+                step()
+        main.wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.outputs = step()
+
+    def __call__(self, ids, targets):
+        self.ids.copy_(ids)
+        self.targets.copy_(targets)
+        self.graph.replay()
+        return self.outputs
 
 
 def check_step(loss, count):

@@ -1,0 +1,58 @@
+"""The graphed training step (one HIP graph per step) against eager steps.
+
+Two copies of one model train on the same batches: one with ``train_step``,
+one with ``GraphedStep`` (capture once, replay). Every replay's loss and
+gradient norm must match the eager step's, and the parameters after the last
+step must agree: a graph node that goes stale after its first replay
+(memsets, host-side values baked in at capture) shows up as a drift here.
+Between replays the test does its own eager work and synchronises.
+checkpoint_chunks on, several encoder and read chunks per step, bf16
+autocast: the cfg5 step's structure at a small size.
+"""
+import copy
+
+import pytest
+import torch
+
+import exploration_amd.model as M
+from exploration_amd.train import GraphedStep, make_optimizer, synthetic_lm_batch, train_step
+
+pytestmark = pytest.mark.gpu
+
+
+def test_graphed_step_matches_eager(device):
+    print("graphed training step vs eager", flush=True)
+    torch.manual_seed(0)
+    cfg = {"vocab_size": 64, "dim": 128, "heads": 2, "block_size": 16, "topk": 64, "arch": "Lx2,G",
+           "ffn_ratio": 4.0}
+    execution = {"checkpoint_chunks": True, "encoder_chunk": 128}
+    eager = M.build_model(cfg, execution=execution, device=device)
+    eager.pos_chunk = 200  # three read chunks of a 512-token sequence
+    graphed = copy.deepcopy(eager)
+    n, warmup, steps = 512, 2, 4
+    batches = [synthetic_lm_batch(64, n, batch=2, seed=s, device=device) for s in range(steps + 1)]
+    batches[2][1][0, 100:] = -100  # a step with fewer supervised positions in one row
+
+    opt_e = make_optimizer(eager, capturable=True)
+    for _ in range(warmup):
+        train_step(eager, opt_e, *batches[0], width=n, autocast_cache=False)
+    want = []
+    for ids, targets in batches[1:]:
+        loss, norm, count = train_step(eager, opt_e, ids, targets, width=n, autocast_cache=False)
+        want.append((loss.item(), norm.item(), count.item()))
+
+    opt_g = make_optimizer(graphed, capturable=True)
+    step = GraphedStep(graphed, opt_g, *batches[0], warmup=warmup)
+    got = []
+    for i, (ids, targets) in enumerate(batches[1:]):
+        loss, norm, count = step(ids, targets)
+        got.append((loss.item(), norm.item(), count.item()))
+        torch.ones(1000, device=device).cumsum(0)  # eager work between replays
+        torch.cuda.synchronize()
+        print(f"  step {i}: eager {want[i]} graphed {got[i]}", flush=True)
+    for (le, ne, ce), (lg, ng, cg) in zip(want, got):
+        assert ce == cg
+        assert lg == pytest.approx(le, rel=1e-4)
+        assert ng == pytest.approx(ne, rel=1e-3)
+    for (name, pe), pg in zip(eager.named_parameters(), graphed.parameters()):
+        torch.testing.assert_close(pg, pe, rtol=1e-4, atol=1e-5, msg=name)
