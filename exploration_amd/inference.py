@@ -225,7 +225,7 @@ class InferenceSession:
         try:
             for lo in range(0, n, self.plan.encoder_chunk):
                 hi = min(n, lo + self.plan.encoder_chunk)
-                x = m.embedding(input_ids[:, lo:hi].to(self.device, non_blocking=True))
+                x = m.embed(input_ids[:, lo:hi].to(self.device, non_blocking=True))
                 for i, layer in enumerate(m.local):
                     prev = halos[i]
                     halos[i] = x[:, -b:].clone()

@@ -122,12 +122,52 @@ class RotaryEmbedding(nn.Module):
         return torch.cat([lo * cos - hi * sin, hi * cos + lo * sin], dim=-1)
 
 
+def _column_sum(t):
+    """Sum of a ``[R, C]`` tensor over its rows (accumulated in at least
+    fp32), in stages of at most 128 rows: every reduction is short, so the
+    library never splits one across workgroups (a split reduction clears its
+    semaphore with a memset, and such graph nodes have gone stale on replays
+    of a captured step)."""
+    dtype = torch.promote_types(t.dtype, torch.float32)
+    acc = None
+    while t.shape[0] > 128:
+        r = t.shape[0] // 128 * 128
+        if r < t.shape[0]:
+            tail = t[r:].sum(0, dtype=dtype)
+            acc = tail if acc is None else acc + tail
+        t = t[:r].reshape(-1, 128, t.shape[1]).sum(1, dtype=dtype)
+    s = t.sum(0, dtype=dtype)
+    return s if acc is None else s + acc
+
+
+class _BiasAdd(torch.autograd.Function):
+    """``y + b`` (b cast to y's dtype, as a fused linear bias under autocast);
+    the bias gradient through ``_column_sum``."""
+
+    @staticmethod
+    def forward(ctx, y, b):
+        ctx.b_dtype = b.dtype
+        return y + b.to(y.dtype)
+
+    @staticmethod
+    def backward(ctx, grad):
+        return grad, _column_sum(grad.reshape(-1, grad.shape[-1])).to(ctx.b_dtype)
+
+
 class FeedForward(nn.Sequential):
-    """Linear -> GELU -> Linear, hidden width round(dim * ratio) (``blocks.py:96-99``)."""
+    """Linear -> GELU -> Linear, hidden width round(dim * ratio) (``blocks.py:96-99``).
+    The biases are added outside the matrix products, so their gradients are
+    the staged column sums of ``_BiasAdd`` (same parameters and state_dict
+    as the reference's ``nn.Sequential``)."""
 
     def __init__(self, dim, ratio):
         hidden = max(1, round(dim * ratio))
         super().__init__(nn.Linear(dim, hidden), nn.GELU(), nn.Linear(hidden, dim))
+
+    def forward(self, x):
+        fc1, act, fc2 = self
+        h = act(_BiasAdd.apply(F.linear(x, fc1.weight), fc1.bias))
+        return _BiasAdd.apply(F.linear(h, fc2.weight), fc2.bias)
 
 
 def _window_attention(q, k, v, mask):
@@ -298,12 +338,28 @@ class StackModel(nn.Module):
         """Tokens -> (x, raw_k, raw_v), raw K/V contiguous ``[B,N,H,hd]``."""
         if input_ids.ndim != 2 or min(input_ids.shape) < 1:
             raise ValueError("input_ids must have nonempty shape [batch, sequence]")
-        x = self.embedding(input_ids)
+        x = self.embed(input_ids)
         for layer in self.local:
             x = layer(x, start=offset)
         raw_k, raw_v = self.raw_kv(x, None)
         # one copy here instead of one per operator call
         return x, raw_k.contiguous(), raw_v.contiguous()
+
+    def embed(self, input_ids):
+        """``self.embedding(ids)`` without the embedding's sort-based backward
+        (a device sort and a look-back segment pass). Vocabularies up to 4096
+        (the byte-level configurations): a one-hot fp32 product, exactly the
+        weight rows forward and a fixed-order, deterministic product backward.
+        Larger ones: a row gather, whose backward adds rows with atomics."""
+        w = self.embedding.weight
+        flat = input_ids.reshape(-1)
+        if w.shape[0] <= 4096:
+            with torch.autocast(w.device.type, enabled=False):
+                onehot = F.one_hot(flat, w.shape[0]).to(w.dtype)
+                x = onehot @ w
+        else:
+            x = w.index_select(0, flat)
+        return x.view(*input_ids.shape, w.shape[1])
 
     def _chunk_size(self, n):
         """Supervised positions per read chunk (``stack.py:315-331``): bounds
@@ -355,14 +411,23 @@ class StackModel(nn.Module):
         elif not 1 <= width <= n:
             raise ValueError("width must lie in [1, sequence length]")
         width = max(int(width), 1)
-        order = torch.arange(n, device=input_ids.device)[None].expand(batch, -1)
-        order = torch.where(sup, order, n).sort(1).values[:, :width]
+        # supervised positions of each row in increasing order, padded with n:
+        # a row prefix sum gives each one its slot, a scatter places it (the
+        # unsupervised ones all land in a discarded extra column). No sort and
+        # no boolean selection: those run decoupled look-back scans, whose
+        # spin-waits have hung in replays of a captured step.
+        idx = torch.arange(n, device=input_ids.device)[None].expand(batch, -1)
+        # (a zero row keeps the prefix sum a per-row scan: one row alone goes
+        # to the library's device-wide scan, which is a look-back scan)
+        count = torch.cat((sup.long(), sup.new_zeros((1, n), dtype=torch.long))).cumsum(1)[:batch]
+        slot = torch.where(sup, count - 1, n)
+        order = torch.full((batch, n + 1), n, device=input_ids.device, dtype=torch.long)
+        order = order.scatter_(1, slot, idx)[:, :width]
         valid = order < n
         safe = order.clamp_max(n - 1)
         pos = torch.where(valid, order + offset, -1)
         labels = targets.gather(1, safe).masked_fill(~valid, -100)
         x, k, v = self.encode(input_ids, offset)
-        rows = torch.arange(batch, device=x.device)[:, None]
         losses, hits = [], []
         step = self._chunk_size(n)
 
@@ -373,7 +438,9 @@ class StackModel(nn.Module):
 
         for lo in range(0, width, step):
             hi = min(lo + step, width)
-            z = x[rows, safe[:, lo:hi]]
+            # gather rows (backward: scatter-add; advanced indexing's backward
+            # sorts and runs a look-back unique pass)
+            z = torch.gather(x, 1, safe[:, lo:hi, None].expand(-1, -1, x.shape[-1]))
             for rd in self.reads:
                 z = self._dense_round(rd, z, k, v, pos[:, lo:hi])
             for j in range(0, hi - lo, self.loss_chunk):

@@ -47,7 +47,12 @@ class GraphedStep:
     ``warmup`` eager steps on a side stream first (they update the model
     like any step), then captures one step without running it. Returns the
     same device tensors as ``train_step``; they are overwritten by the next
-    call."""
+    call, which returns after the replay has finished.
+
+    The model's step is written so that the graph holds no library kernel
+    with a decoupled look-back (device-wide sort, unique, select or a
+    one-row scan): such kernels spin on flags other workgroups set and have
+    hung in replays here."""
 
     def __init__(self, model, optimizer, ids, targets, clip_grad=1.0, precision="bf16", warmup=3):
         if not ids.is_cuda:
@@ -75,6 +80,10 @@ class GraphedStep:
         self.ids.copy_(ids)
         self.targets.copy_(targets)
         self.graph.replay()
+        # one replay at a time: replays queued back to back have hung here in
+        # a library kernel whose workgroups spin on each other's flags (a
+        # look-back scan); waiting costs a fraction of a percent of a step
+        torch.cuda.current_stream(self.ids.device).synchronize()
         return self.outputs
 
 

@@ -7,7 +7,9 @@ step must agree: a graph node that goes stale after its first replay
 (memsets, host-side values baked in at capture) shows up as a drift here.
 Between replays the test does its own eager work and synchronises.
 checkpoint_chunks on, several encoder and read chunks per step, bf16
-autocast: the cfg5 step's structure at a small size.
+autocast: the cfg5 step's structure at a small size; and the cfg5 widths
+(dim 1024, FFN 4096) over 8192 tokens in one chunk, where the reductions
+over all rows are long (two layers to keep it quick).
 """
 import copy
 
@@ -56,3 +58,28 @@ def test_graphed_step_matches_eager(device):
         assert ng == pytest.approx(ne, rel=1e-3)
     for (name, pe), pg in zip(eager.named_parameters(), graphed.parameters()):
         torch.testing.assert_close(pg, pe, rtol=1e-4, atol=1e-5, msg=name)
+
+
+def test_graphed_step_matches_eager_full_width(device):
+    """Every replay bitwise equal to the eager step at cfg5 widths with whole
+    8192-token chunks: long reductions (the FFN bias gradients over 8192
+    rows) once recorded memset nodes that went stale from the third replay."""
+    print("graphed training step vs eager, cfg5 widths, whole chunks", flush=True)
+    cfg = dict(M.STACK_100M, arch="Lx1,G")
+    execution = {"checkpoint_chunks": True, "encoder_chunk": 8192, "query_chunk": 8192, "loss_chunk": 8192}
+    ids, targets = synthetic_lm_batch(cfg["vocab_size"], 8192, batch=1, seed=0, device=device)
+    runs = {}
+    for mode in ("eager", "graph"):
+        torch.manual_seed(0)
+        m = M.build_model(cfg, execution=execution, device=device)
+        opt = make_optimizer(m, capturable=True)
+        if mode == "eager":
+            losses = [train_step(m, opt, ids, targets, width=8192, autocast_cache=False)[0].item() for _ in range(7)]
+        else:
+            step = GraphedStep(m, opt, ids, targets, warmup=1)
+            losses = [None] + [step(ids, targets)[0].item() for _ in range(6)]
+        runs[mode] = (losses, [p.detach().clone() for p in m.parameters()])
+        print(f"  {mode}: {losses}", flush=True)
+    assert runs["graph"][0][1:] == runs["eager"][0][1:]
+    for pe, pg in zip(runs["eager"][1], runs["graph"][1]):
+        assert torch.equal(pe, pg)
