@@ -102,3 +102,42 @@ def synthetic_lm_batch(vocab, length, batch=1, seed=0, device="cpu"):
     targets = torch.roll(ids, -1, 1)
     targets[:, -1] = -100
     return ids.to(device), targets.to(device)
+
+
+def main(argv=None):
+    """``python -m exploration_amd.train``: the cfg5 training step (a
+    stack_100m-shaped model, random init, batch 1, length 8192, every position
+    supervised) as one HIP graph, replayed ``--steps`` times; prints tokens/s.
+    ``--whole-chunks`` uses whole-sequence encoder, read and loss chunks
+    instead of the config's (1024, auto, 128)."""
+    import argparse
+    import time
+
+    from .model import STACK_100M, build_model
+
+    p = argparse.ArgumentParser(description=main.__doc__)
+    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--length", type=int, default=8192)
+    p.add_argument("--whole-chunks", action="store_true")
+    args = p.parse_args(argv)
+    n = args.length
+    runtime = ({"checkpoint_chunks": True, "encoder_chunk": n, "query_chunk": n, "loss_chunk": n}
+               if args.whole_chunks else
+               {"checkpoint_chunks": True, "encoder_chunk": 1024, "query_chunk": 0, "loss_chunk": 128})
+    torch.manual_seed(0)
+    model = build_model(STACK_100M, execution=runtime, device="cuda")
+    opt = make_optimizer(model, capturable=True)
+    ids, targets = synthetic_lm_batch(STACK_100M["vocab_size"], n, batch=1, seed=0, device="cuda")
+    step = GraphedStep(model, opt, ids, targets, warmup=1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        loss = step(ids, targets)[0]
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    print(f"runtime {runtime}: {dt * 1e3:.2f} ms per step, {n / dt:.0f} tokens/s, loss {float(loss):.4f}",
+          flush=True)
+
+
+if __name__ == "__main__":
+    main()
