@@ -11,6 +11,7 @@
 #include "../../include/st_attn.h"
 #include "dense.h"
 #include "sparse.h"
+#include "halo.h"
 
 namespace {
 
@@ -343,3 +344,60 @@ int st_sparse_fwd(int dtype, int64_t batch, int64_t queries, int64_t heads, int6
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// local-block window attention
+
+static int fill_halo(st::HaloArgs& a, const char* who, int dtype, int64_t batch, int64_t groups, int64_t block_size,
+                     int64_t heads, int64_t head_dim, int64_t n, int64_t start, int64_t first_key, const void* qkv,
+                     const float* cos_t, const float* sin_t) {
+  if (int r = check_dtype(dtype)) return r;
+  if (batch < 1 || groups < 1 || block_size < 1 || heads < 1 || head_dim < 2 || n < 1)
+    return fail(ST_EINVAL, "%s: dimensions must be positive", who);
+  if (n > groups * block_size || n <= (groups - 1) * block_size)
+    return fail(ST_EINVAL, "%s: n = %lld rows need ceil(n / block_size) = groups blocks", who, (long long)n);
+  if (!st::halo_supported((int)block_size, (int)head_dim))
+    return fail(ST_EUNSUPPORTED, "%s: no kernel for block_size %lld, head_dim %lld", who, (long long)block_size,
+                (long long)head_dim);
+  if (batch * (groups + 1) * heads >= (int64_t(1) << 31) || start < 0 || first_key < 0 || first_key > start)
+    return fail(ST_EINVAL, "%s: grid or positions out of range", who);
+  if (!qkv || !cos_t || !sin_t) return fail(ST_EINVAL, "%s: null pointer", who);
+  a = st::HaloArgs{};
+  a.B = (int)batch; a.G = (int)groups; a.b = (int)block_size; a.H = (int)heads; a.hd = (int)head_dim;
+  a.n = (int)n; a.start = start; a.first_key = first_key;
+  a.scale = 1.f / sqrtf((float)head_dim);
+  a.qkv = qkv; a.cos_t = cos_t; a.sin_t = sin_t;
+  return ST_OK;
+}
+
+int st_halo_supported(int dtype, int64_t block_size, int64_t head_dim) {
+  return (dtype == ST_DTYPE_F32 || dtype == ST_DTYPE_F16 || dtype == ST_DTYPE_BF16) &&
+         st::halo_supported((int)block_size, (int)head_dim);
+}
+
+int st_halo_attn_fwd(int dtype, int64_t batch, int64_t groups, int64_t block_size, int64_t heads,
+                     int64_t head_dim, int64_t n, int64_t start, int64_t first_key, const void* qkv,
+                     const float* cos_t, const float* sin_t, void* out, void* stream) {
+  st::HaloArgs a;
+  if (int r = fill_halo(a, "st_halo_attn_fwd", dtype, batch, groups, block_size, heads, head_dim, n, start,
+                        first_key, qkv, cos_t, sin_t))
+    return r;
+  if (!out) return fail(ST_EINVAL, "st_halo_attn_fwd: null pointer");
+  a.out = out;
+  return launched(st::launch_halo_fwd(dtype, a, as_stream(stream)), "st_halo_attn_fwd");
+}
+
+int st_halo_attn_bwd(int dtype, int64_t batch, int64_t groups, int64_t block_size, int64_t heads,
+                     int64_t head_dim, int64_t n, int64_t start, int64_t first_key, const void* qkv,
+                     const float* cos_t, const float* sin_t, const void* out, const void* dout, void* dqkv,
+                     void* stream) {
+  st::HaloArgs a;
+  if (int r = fill_halo(a, "st_halo_attn_bwd", dtype, batch, groups, block_size, heads, head_dim, n, start,
+                        first_key, qkv, cos_t, sin_t))
+    return r;
+  if (!out || !dout || !dqkv) return fail(ST_EINVAL, "st_halo_attn_bwd: null pointer");
+  a.out = const_cast<void*>(out);
+  a.dout = dout;
+  a.dqkv = dqkv;
+  return launched(st::launch_halo_bwd(dtype, a, as_stream(stream)), "st_halo_attn_bwd");
+}

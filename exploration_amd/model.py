@@ -25,6 +25,7 @@ from torch.nn import functional as F
 from torch.utils.checkpoint import checkpoint
 
 from .attention import dense_attention
+from .local import halo_attention, halo_supported
 from .sparse import TensorPages, sparse_attention
 
 
@@ -197,6 +198,9 @@ class HaloMemoryBlock(nn.Module):
         self.out = nn.Linear(dim, dim, bias=False)
         self.ffn_norm = nn.LayerNorm(dim)
         self.ffn = FeedForward(dim, ffn_ratio)
+        # the fused window-attention kernels for supported GPU shapes (False:
+        # always the PyTorch attention below)
+        self.fused = True
 
     def forward_chunk(self, x, previous=None, start=0):
         batch, n, dim = x.shape
@@ -211,7 +215,13 @@ class HaloMemoryBlock(nn.Module):
                 raise ValueError("previous halo must contain exactly one block")
             first_key = max(0, start - b)
         seq = torch.cat((previous, F.pad(x, (0, 0, 0, groups * b - n))), 1)
-        qkv = self.qkv(self.attn_norm(seq)).reshape(batch, groups + 1, b, 3, self.heads, self.hd)
+        qkv = self.qkv(self.attn_norm(seq))
+        if self.fused and halo_supported(qkv, b, self.hd):
+            # rotary, window and attention in one kernel per direction
+            ctx = halo_attention(qkv, self.rope, b, self.heads, n, start, first_key)
+            y = x + self.out(ctx)
+            return y + self.ffn(self.ffn_norm(y))
+        qkv = qkv.reshape(batch, groups + 1, b, 3, self.heads, self.hd)
         q, k, v = qkv.unbind(3)
         q = self.rope(q[:, 1:], torch.arange(b, device=x.device))
         kw = self.rope(torch.cat((k[:, :-1], k[:, 1:]), 2), torch.arange(-b, b, device=x.device))

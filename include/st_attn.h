@@ -142,6 +142,27 @@ int st_sparse_fwd(int dtype, int64_t batch, int64_t queries, int64_t heads, int6
                   int64_t* ids, float* top_scores, float* log_zr, float* lse, void* workspace,
                   size_t workspace_bytes, void* stream);
 
+/* Two-block window attention of the model's local blocks (no st.ops
+ * counterpart: the reference computes it with torch's scaled dot-product
+ * attention, st/models/blocks.py:131-160, after the rotary embedding of
+ * blocks.py:76-93). qkv [B, (G+1)*b, 3, H, hd] is the projection output of
+ * [previous block ++ the chunk padded to G*b rows]; query block g attends to
+ * raw blocks g and g+1, key kk visible to query i when kk <= i + b and its
+ * absolute position lies in [first_key, start + n). cos_t / sin_t [2b, hd/2]
+ * float: the rotary cos/sin of positions -b..b-1, as the reference computes
+ * them and rounded to dtype. out [B, n, H, hd] (dtype) receives the first n
+ * rows. 1 if (block_size, head_dim) has a kernel, else 0. */
+int st_halo_supported(int dtype, int64_t block_size, int64_t head_dim);
+int st_halo_attn_fwd(int dtype, int64_t batch, int64_t groups, int64_t block_size, int64_t heads,
+                     int64_t head_dim, int64_t n, int64_t start, int64_t first_key, const void* qkv,
+                     const float* cos_t, const float* sin_t, void* out, void* stream);
+/* Backward: writes every element of dqkv (same layout as qkv) from dout
+ * [B, n, H, hd] and the forward's out; deterministic (no atomics). */
+int st_halo_attn_bwd(int dtype, int64_t batch, int64_t groups, int64_t block_size, int64_t heads,
+                     int64_t head_dim, int64_t n, int64_t start, int64_t first_key, const void* qkv,
+                     const float* cos_t, const float* sin_t, const void* out, const void* dout, void* dqkv,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif
