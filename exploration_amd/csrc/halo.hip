@@ -28,6 +28,7 @@
 // chunk: its dq is zero.
 #include "common.h"
 #include "halo.h"
+#include "tile.h"
 
 namespace st {
 
@@ -249,6 +250,332 @@ __global__ __launch_bounds__(64) void halo_bwd_kernel(HaloArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// head_dim 64 (the stack_100m shape): register-blocked variants. The loops
+// above load both operands of every FMA from LDS; these keep one operand in
+// registers and read the other as 16-byte broadcasts.
+//  * row phases (scores, dP): lane = key kk + W * slice; the lane holds its
+//    key's K (and V) slice of 64 / LPK dims, every query (dO) row is a
+//    broadcast read, the LPK slice sums meet through cross-lane adds;
+//  * column phases (output, dq, dk, dv): lane = head-dim column d; the lane
+//    holds its column of V, K, Q or dO, the P / dS rows are broadcast reads.
+// The rotary transposes of dq and dk pair column d with d + 32 and go
+// through an LDS scratch tile.
+template <int B_>
+struct Halo64 {
+  static constexpr int HD = 64, HALF = 32, W = 2 * B_, LPK = 64 / W, SL = HD / LPK;
+  static constexpr int LD = HD + 4, PS = W + 4;  // 16-byte aligned rows
+  static constexpr int NP = B_ * HALF / 64;
+  static_assert(LPK >= 1 && SL % 4 == 0 && W % 4 == 0, "shape");
+};
+
+// Stage query block g (rotated), its window keys (rotated) and values, as
+// fp32. Every global load of the unit is issued before the first store
+// (16-byte vectors, clamped indices instead of predicates), so the wave waits
+// for one memory round trip, not one per element.
+template <typename T, int B_>
+__device__ __forceinline__ void stage64(const HaloArgs& a, const T* qkv, int64_t row0, int h, int g, float* qs,
+                                        float* ks, float* vs) {
+  typedef Halo64<B_> S;
+  typedef typename Vec16<T>::type V;
+  constexpr int E = Vec16<T>::n, VPR = S::HD / E, HV = VPR / 2, E4 = E / 4;
+  constexpr int NQ = B_ * HV, NK = S::W * HV, NV = S::W * VPR;
+  constexpr int TQ = (NQ + 63) / 64, TK = (NK + 63) / 64, TV = (NV + 63) / 64;
+  const int lane = threadIdx.x;
+  const int64_t dim = (int64_t)a.H * S::HD;
+  auto src = [&](int r, int slot, int d) { return qkv + ((row0 + r) * 3 + slot) * dim + (int64_t)h * S::HD + d; };
+  V ql[TQ], qh[TQ], kl[TK], kh[TK], vv[TV];
+  f32x4 qc[TQ][E4], qn[TQ][E4], kc[TK][E4], kn[TK][E4];
+#pragma unroll
+  for (int t = 0; t < TQ; ++t) {
+    const int e = min(lane + 64 * t, NQ - 1), i = e / HV, c = e % HV;
+    ql[t] = load_vec<V>(src((g + 1) * B_ + i, 0, c * E));
+    qh[t] = load_vec<V>(src((g + 1) * B_ + i, 0, c * E + S::HALF));
+#pragma unroll
+    for (int u = 0; u < E4; ++u) {
+      qc[t][u] = load_vec<f32x4>(a.cos_t + (B_ + i) * S::HALF + c * E + 4 * u);
+      qn[t][u] = load_vec<f32x4>(a.sin_t + (B_ + i) * S::HALF + c * E + 4 * u);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TK; ++t) {
+    const int e = min(lane + 64 * t, NK - 1), kk = e / HV, c = e % HV;
+    kl[t] = load_vec<V>(src(g * B_ + kk, 1, c * E));
+    kh[t] = load_vec<V>(src(g * B_ + kk, 1, c * E + S::HALF));
+#pragma unroll
+    for (int u = 0; u < E4; ++u) {
+      kc[t][u] = load_vec<f32x4>(a.cos_t + kk * S::HALF + c * E + 4 * u);
+      kn[t][u] = load_vec<f32x4>(a.sin_t + kk * S::HALF + c * E + 4 * u);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TV; ++t) {
+    const int e = min(lane + 64 * t, NV - 1), kk = e / VPR, c = e % VPR;
+    vv[t] = load_vec<V>(src(g * B_ + kk, 2, c * E));
+  }
+#pragma unroll
+  for (int t = 0; t < TQ; ++t) {
+    const int e = lane + 64 * t, i = min(e, NQ - 1) / HV, c = e % HV;
+    if (e >= NQ) break;
+#pragma unroll
+    for (int u = 0; u < E; ++u) {
+      const float lo = to_float<T>(ql[t][u]), hi = to_float<T>(qh[t][u]);
+      const float cs = qc[t][u / 4][u % 4], sn = qn[t][u / 4][u % 4];
+      qs[i * S::LD + c * E + u] = round_to<T>(lo * cs - hi * sn);
+      qs[i * S::LD + c * E + u + S::HALF] = round_to<T>(hi * cs + lo * sn);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TK; ++t) {
+    const int e = lane + 64 * t, kk = min(e, NK - 1) / HV, c = e % HV;
+    if (e >= NK) break;
+#pragma unroll
+    for (int u = 0; u < E; ++u) {
+      const float lo = to_float<T>(kl[t][u]), hi = to_float<T>(kh[t][u]);
+      const float cs = kc[t][u / 4][u % 4], sn = kn[t][u / 4][u % 4];
+      ks[kk * S::LD + c * E + u] = round_to<T>(lo * cs - hi * sn);
+      ks[kk * S::LD + c * E + u + S::HALF] = round_to<T>(hi * cs + lo * sn);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TV; ++t) {
+    const int e = lane + 64 * t, kk = min(e, NV - 1) / VPR, c = e % VPR;
+    if (e >= NV) break;
+#pragma unroll
+    for (int u = 0; u < E; ++u) vs[kk * S::LD + c * E + u] = to_float<T>(vv[t][u]);
+  }
+}
+
+// dO and O rows of query block g as fp32 (zero beyond the n real rows), all
+// loads first.
+template <typename T, int B_>
+__device__ __forceinline__ void stage_rows64(const HaloArgs& a, int bi, int h, int g, float* dos, float* os) {
+  typedef Halo64<B_> S;
+  typedef typename Vec16<T>::type V;
+  constexpr int E = Vec16<T>::n, VPR = S::HD / E, N = B_ * VPR, TT = (N + 63) / 64;
+  const int lane = threadIdx.x;
+  const int64_t dim = (int64_t)a.H * S::HD;
+  const T* dout = reinterpret_cast<const T*>(a.dout);
+  const T* out = reinterpret_cast<const T*>(a.out);
+  V gv[TT], ov[TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    const int e = min(lane + 64 * t, N - 1), i = e / VPR, c = e % VPR;
+    const int row = min(g * B_ + i, a.n - 1);
+    const int64_t o = ((int64_t)bi * a.n + row) * dim + (int64_t)h * S::HD + c * E;
+    gv[t] = load_vec<V>(dout + o);
+    ov[t] = load_vec<V>(out + o);
+  }
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    const int e = lane + 64 * t, i = min(e, N - 1) / VPR, c = e % VPR;
+    if (e >= N) break;
+    const bool real = g * B_ + i < a.n;
+#pragma unroll
+    for (int u = 0; u < E; ++u) {
+      dos[i * S::LD + c * E + u] = real ? to_float<T>(gv[t][u]) : 0.f;
+      os[i * S::LD + c * E + u] = real ? to_float<T>(ov[t][u]) : 0.f;
+    }
+  }
+}
+
+// Sum over the LPK lanes holding slices of one key (lanes kk + W * slice).
+template <int W>
+__device__ __forceinline__ float slice_sum(float x) {
+#pragma unroll
+  for (int off = W; off < 64; off <<= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+template <int N>
+__device__ __forceinline__ float dot_bcast(const float* row, const float (&reg)[N]) {
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < N; c += 4) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(row + c);
+    s += v[0] * reg[c] + v[1] * reg[c + 1] + v[2] * reg[c + 2] + v[3] * reg[c + 3];
+  }
+  return s;
+}
+
+// Masked scores of query block g (row phase) and their row softmax, into ps.
+template <int B_>
+__device__ __forceinline__ void probs64(const HaloArgs& a, int g, const float* qs, const float (&kreg)[Halo64<B_>::SL],
+                                        float* ps) {
+  typedef Halo64<B_> S;
+  const int lane = threadIdx.x, kk = lane % S::W, sl = lane / S::W;
+  const int64_t kp = a.start + (int64_t)(g - 1) * B_ + kk;
+  const bool key_ok = kp >= a.first_key && kp < a.start + a.n;
+#pragma unroll 4
+  for (int i = 0; i < B_; ++i) {
+    const float s = slice_sum<S::W>(dot_bcast(qs + i * S::LD + sl * S::SL, kreg));
+    if (sl == 0) ps[i * S::PS + kk] = (key_ok && kk <= i + B_) ? s * a.scale : kNegInf;
+  }
+  __syncthreads();
+  for (int i = lane; i < B_; i += 64) {
+    float m = kNegInf;
+    for (int k2 = 0; k2 < S::W; ++k2) m = fmaxf(m, ps[i * S::PS + k2]);
+    float sum = 0.f;
+    for (int k2 = 0; k2 < S::W; ++k2) {
+      const float p = m == kNegInf ? 0.f : __expf(ps[i * S::PS + k2] - m);
+      ps[i * S::PS + k2] = p;
+      sum += p;
+    }
+    const float inv = sum > 0.f ? 1.f / sum : 0.f;
+    for (int k2 = 0; k2 < S::W; ++k2) ps[i * S::PS + k2] *= inv;
+  }
+  __syncthreads();
+}
+
+template <typename T, int B_>
+__global__ __launch_bounds__(64) void halo_fwd64_kernel(HaloArgs a) {
+  typedef Halo64<B_> S;
+  __shared__ __attribute__((aligned(16))) float qs[B_ * S::LD], ks[S::W * S::LD], vs[S::W * S::LD], ps[B_ * S::PS];
+  const int lane = threadIdx.x;
+  const int h = (int)(blockIdx.x % (unsigned)a.H);
+  const int g = (int)((blockIdx.x / (unsigned)a.H) % (unsigned)a.G);
+  const int bi = (int)(blockIdx.x / ((unsigned)a.H * (unsigned)a.G));
+  const int64_t row0 = (int64_t)bi * (a.G + 1) * B_;
+  stage64<T, B_>(a, reinterpret_cast<const T*>(a.qkv), row0, h, g, qs, ks, vs);
+  __syncthreads();
+  float kreg[S::SL];
+  {
+    const int kk = lane % S::W, sl = lane / S::W;
+#pragma unroll
+    for (int c = 0; c < S::SL; ++c) kreg[c] = ks[kk * S::LD + sl * S::SL + c];
+  }
+  probs64<B_>(a, g, qs, kreg, ps);
+  float vcol[S::W];
+#pragma unroll
+  for (int kk = 0; kk < S::W; ++kk) vcol[kk] = vs[kk * S::LD + lane];
+  T* out = reinterpret_cast<T*>(a.out);
+  const int64_t dim = (int64_t)a.H * S::HD;
+#pragma unroll 4
+  for (int i = 0; i < B_; ++i) {
+    const int t = g * B_ + i;
+    if (t >= a.n) break;
+    out[((int64_t)bi * a.n + t) * dim + (int64_t)h * S::HD + lane] = from_float<T>(dot_bcast(ps + i * S::PS, vcol));
+  }
+}
+
+template <typename T, int B_>
+__global__ __launch_bounds__(64) void halo_bwd64_kernel(HaloArgs a) {
+  typedef Halo64<B_> S;
+  __shared__ __attribute__((aligned(16))) float qs[B_ * S::LD], ks[S::W * S::LD], vs[S::W * S::LD];
+  __shared__ __attribute__((aligned(16))) float dos[B_ * S::LD], scr[B_ * S::LD], ps[B_ * S::PS], dss[B_ * S::PS];
+  __shared__ float delta[B_];
+  const int lane = threadIdx.x;
+  const int h = (int)(blockIdx.x % (unsigned)a.H);
+  const int r = (int)((blockIdx.x / (unsigned)a.H) % (unsigned)(a.G + 1));
+  const int bi = (int)(blockIdx.x / ((unsigned)a.H * (unsigned)(a.G + 1)));
+  const int64_t row0 = (int64_t)bi * (a.G + 1) * B_;
+  const int64_t dim = (int64_t)a.H * S::HD;
+  const T* qkv = reinterpret_cast<const T*>(a.qkv);
+  T* dqkv = reinterpret_cast<T*>(a.dqkv);
+  auto at = [&](int row, int slot, int d) { return ((row0 + row) * 3 + slot) * dim + (int64_t)h * S::HD + d; };
+  const int kk_l = lane % S::W, sl = lane / S::W;
+
+  float dk_lo[S::NP], dk_hi[S::NP], dv[B_];
+#pragma unroll
+  for (int p = 0; p < S::NP; ++p) dk_lo[p] = dk_hi[p] = 0.f;
+#pragma unroll
+  for (int i = 0; i < B_; ++i) dv[i] = 0.f;
+
+  for (int role = 0; role < 2; ++role) {
+    const int g = role == 0 ? r - 1 : r;  // role 0: own block of query block r-1; role 1: previous of query block r
+    if (g < 0 || g >= a.G) continue;      // uniform over the wave
+    __syncthreads();
+    stage64<T, B_>(a, qkv, row0, h, g, qs, ks, vs);
+    // dO rows and delta = rowsum(dO * O) (O read once, into the scratch tile)
+    stage_rows64<T, B_>(a, bi, h, g, dos, scr);
+    __syncthreads();
+    for (int i = lane; i < B_; i += 64) {
+      float s = 0.f;
+      for (int d = 0; d < S::HD; ++d) s += dos[i * S::LD + d] * scr[i * S::LD + d];
+      delta[i] = s;
+    }
+    float kreg[S::SL], vreg[S::SL];
+#pragma unroll
+    for (int c = 0; c < S::SL; ++c) {
+      kreg[c] = ks[kk_l * S::LD + sl * S::SL + c];
+      vreg[c] = vs[kk_l * S::LD + sl * S::SL + c];
+    }
+    probs64<B_>(a, g, qs, kreg, ps);  // (its barriers also publish delta)
+    // dS = P (dP - delta) with dP = dO V^T (row phase)
+#pragma unroll 4
+    for (int i = 0; i < B_; ++i) {
+      const float dp = slice_sum<S::W>(dot_bcast(dos + i * S::LD + sl * S::SL, vreg));
+      if (sl == 0) {
+        const float pv = ps[i * S::PS + kk_l];
+        dss[i * S::PS + kk_l] = pv * (dp - delta[i]);
+      }
+    }
+    __syncthreads();
+    // column phase, lane = d
+    const int d = lane;
+    if (role == 0) {
+      float kcol[S::W];
+#pragma unroll
+      for (int kk = 0; kk < S::W; ++kk) kcol[kk] = ks[kk * S::LD + d];
+#pragma unroll 4
+      for (int i = 0; i < B_; ++i) scr[i * S::LD + d] = a.scale * dot_bcast(dss + i * S::PS, kcol);
+    }
+    const int kk0 = role == 0 ? B_ : 0;
+    float qcol[B_], docol[B_];
+#pragma unroll
+    for (int i = 0; i < B_; ++i) {
+      qcol[i] = qs[i * S::LD + d];
+      docol[i] = dos[i * S::LD + d];
+    }
+    // dv of this role's window rows; dk (before its rotary) into ks rows
+    // kk0.. (the keys are no longer read in this role)
+    __syncthreads();
+#pragma unroll
+    for (int i2 = 0; i2 < B_; ++i2) {
+      const int kk = kk0 + i2;
+      float sv = 0.f, sk = 0.f;
+#pragma unroll
+      for (int i = 0; i < B_; ++i) {
+        sv += ps[i * S::PS + kk] * docol[i];
+        sk += dss[i * S::PS + kk] * qcol[i];
+      }
+      dv[i2] += sv;
+      ks[kk * S::LD + d] = a.scale * sk;
+    }
+    __syncthreads();
+    if (role == 0) {
+      for (int e = lane; e < B_ * S::HALF; e += 64) {
+        const int i = e / S::HALF, j = e % S::HALF;
+        const float lo = scr[i * S::LD + j], hi = scr[i * S::LD + j + S::HALF];
+        const float c = a.cos_t[(B_ + i) * S::HALF + j], s = a.sin_t[(B_ + i) * S::HALF + j];
+        dqkv[at(r * B_ + i, 0, j)] = from_float<T>(lo * c + hi * s);
+        dqkv[at(r * B_ + i, 0, j + S::HALF)] = from_float<T>(hi * c - lo * s);
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < S::NP; ++p) {
+      const int e = lane + 64 * p;
+      const int i2 = e / S::HALF, j = e % S::HALF, kk = kk0 + i2;
+      const float lo = ks[kk * S::LD + j], hi = ks[kk * S::LD + j + S::HALF];
+      const float c = a.cos_t[kk * S::HALF + j], s = a.sin_t[kk * S::HALF + j];
+      dk_lo[p] += lo * c + hi * s;
+      dk_hi[p] += hi * c - lo * s;
+    }
+  }
+  if (r == 0) {
+    for (int e = lane; e < B_ * S::HD; e += 64) dqkv[at(e / S::HD, 0, e % S::HD)] = from_float<T>(0.f);
+  }
+#pragma unroll
+  for (int p = 0; p < S::NP; ++p) {
+    const int e = lane + 64 * p;
+    const int i2 = e / S::HALF, j = e % S::HALF;
+    dqkv[at(r * B_ + i2, 1, j)] = from_float<T>(dk_lo[p]);
+    dqkv[at(r * B_ + i2, 1, j + S::HALF)] = from_float<T>(dk_hi[p]);
+  }
+#pragma unroll
+  for (int i2 = 0; i2 < B_; ++i2) dqkv[at(r * B_ + i2, 2, lane)] = from_float<T>(dv[i2]);
+}
+
 template <int B_, int HD>
 constexpr size_t bwd_lds() {
   typedef HaloShape<B_, HD> S;
@@ -261,8 +588,13 @@ template <typename T, bool BWD>
 hipError_t dispatch(const HaloArgs& a, hipStream_t s) {
   const unsigned units = (unsigned)((int64_t)a.B * (BWD ? a.G + 1 : a.G) * a.H);
   auto go = [&]<int B_, int HD>() {
-    if constexpr (BWD) hipLaunchKernelGGL((halo_bwd_kernel<T, B_, HD>), dim3(units), dim3(64), 0, s, a);
-    else hipLaunchKernelGGL((halo_fwd_kernel<T, B_, HD>), dim3(units), dim3(64), 0, s, a);
+    if constexpr (HD == 64) {
+      if constexpr (BWD) hipLaunchKernelGGL((halo_bwd64_kernel<T, B_>), dim3(units), dim3(64), 0, s, a);
+      else hipLaunchKernelGGL((halo_fwd64_kernel<T, B_>), dim3(units), dim3(64), 0, s, a);
+    } else {
+      if constexpr (BWD) hipLaunchKernelGGL((halo_bwd_kernel<T, B_, HD>), dim3(units), dim3(64), 0, s, a);
+      else hipLaunchKernelGGL((halo_fwd_kernel<T, B_, HD>), dim3(units), dim3(64), 0, s, a);
+    }
     return hipGetLastError();
   };
 #define ST_HALO_CASE(BB, DD) \

@@ -21,7 +21,7 @@ from tests.helpers import assert_close
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(16, 64, 4), (8, 32, 2), (4, 128, 1), (16, 128, 2), (32, 32, 3), (4, 32, 2), (8, 128, 1)]
+SHAPES = [(16, 64, 4), (8, 64, 2), (4, 64, 3), (8, 32, 2), (4, 128, 1), (16, 128, 2), (32, 32, 3), (4, 32, 2), (8, 128, 1)]
 
 
 def _block(dim, heads, b, device, dtype):
