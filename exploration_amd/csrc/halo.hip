@@ -412,17 +412,30 @@ __device__ __forceinline__ void probs64(const HaloArgs& a, int g, const float* q
     if (sl == 0) ps[i * S::PS + kk] = (key_ok && kk <= i + B_) ? s * a.scale : kNegInf;
   }
   __syncthreads();
-  for (int i = lane; i < B_; i += 64) {
+  // row softmax, LPR adjacent lanes per row (each holds W / LPR scores)
+  constexpr int LPR = 64 / B_ < S::W ? 64 / B_ : S::W, PER = S::W / LPR;
+  if (lane < B_ * LPR) {
+    const int i = lane / LPR, part = lane % LPR;
+    float v[PER];
     float m = kNegInf;
-    for (int k2 = 0; k2 < S::W; ++k2) m = fmaxf(m, ps[i * S::PS + k2]);
-    float sum = 0.f;
-    for (int k2 = 0; k2 < S::W; ++k2) {
-      const float p = m == kNegInf ? 0.f : __expf(ps[i * S::PS + k2] - m);
-      ps[i * S::PS + k2] = p;
-      sum += p;
+#pragma unroll
+    for (int t = 0; t < PER; ++t) {
+      v[t] = ps[i * S::PS + part + LPR * t];
+      m = fmaxf(m, v[t]);
     }
+#pragma unroll
+    for (int off = 1; off < LPR; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    float sum = 0.f;
+#pragma unroll
+    for (int t = 0; t < PER; ++t) {
+      v[t] = m == kNegInf ? 0.f : __expf(v[t] - m);
+      sum += v[t];
+    }
+#pragma unroll
+    for (int off = 1; off < LPR; off <<= 1) sum += __shfl_xor(sum, off, 64);
     const float inv = sum > 0.f ? 1.f / sum : 0.f;
-    for (int k2 = 0; k2 < S::W; ++k2) ps[i * S::PS + k2] *= inv;
+#pragma unroll
+    for (int t = 0; t < PER; ++t) ps[i * S::PS + part + LPR * t] = v[t] * inv;
   }
   __syncthreads();
 }
@@ -489,10 +502,20 @@ __global__ __launch_bounds__(64) void halo_bwd64_kernel(HaloArgs a) {
     // dO rows and delta = rowsum(dO * O) (O read once, into the scratch tile)
     stage_rows64<T, B_>(a, bi, h, g, dos, scr);
     __syncthreads();
-    for (int i = lane; i < B_; i += 64) {
-      float s = 0.f;
-      for (int d = 0; d < S::HD; ++d) s += dos[i * S::LD + d] * scr[i * S::LD + d];
-      delta[i] = s;
+    {
+      // delta = rowsum(dO * O): 64 / B_ adjacent lanes per row
+      constexpr int LR = 64 / B_, DL = S::HD / LR;
+      const int i = lane / LR, part = lane % LR;
+      float sd = 0.f;
+#pragma unroll
+      for (int c = 0; c < DL; c += 4) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(dos + i * S::LD + part * DL + c);
+        const f32x4 y = *reinterpret_cast<const f32x4*>(scr + i * S::LD + part * DL + c);
+        sd += x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
+      }
+#pragma unroll
+      for (int off = 1; off < LR; off <<= 1) sd += __shfl_xor(sd, off, 64);
+      if (part == 0) delta[i] = sd;
     }
     float kreg[S::SL], vreg[S::SL];
 #pragma unroll
