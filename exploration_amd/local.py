@@ -22,7 +22,9 @@ def rope_tables(rope, b, dtype, device):
     key = (b, dtype, str(device), float(rope.base), rope.head_dim)
     found = _tables.get(key)
     if found is None:
-        with torch.autocast(torch.device(device).type, enabled=False):
+        # ordinary tensors even when first built under inference_mode: the
+        # cache serves later training steps too
+        with torch.inference_mode(False), torch.autocast(torch.device(device).type, enabled=False):
             freq = rope.base ** (-rope.frequency_index.to(device).float() / rope.head_dim)
             angle = torch.arange(-b, b, device=device).float()[:, None] * freq
             found = (angle.cos().to(dtype).float().contiguous(), angle.sin().to(dtype).float().contiguous())
@@ -49,7 +51,8 @@ class _HaloAttention(torch.autograd.Function):
         _lib.check(lib.st_halo_attn_fwd(code, batch, groups, b, heads, hd, n, start, first_key, _lib.ptr(qkv),
                                         _lib.ptr(cos_t), _lib.ptr(sin_t), _lib.ptr(out), _lib.stream_of(qkv)),
                    lib)
-        ctx.save_for_backward(qkv, cos_t, sin_t, out)
+        ctx.save_for_backward(qkv, out)
+        ctx.tables = (cos_t, sin_t)  # constants: not saved as autograd inputs
         ctx.args = (code, batch, groups, b, heads, hd, n, start, first_key)
         return out
 
@@ -57,7 +60,8 @@ class _HaloAttention(torch.autograd.Function):
     @once_differentiable
     def backward(ctx, dout):
         lib = _lib.load()
-        qkv, cos_t, sin_t, out = ctx.saved_tensors
+        qkv, out = ctx.saved_tensors
+        cos_t, sin_t = ctx.tables
         dout = dout.to(qkv.dtype).contiguous()
         dqkv = torch.empty_like(qkv)
         _lib.check(lib.st_halo_attn_bwd(*ctx.args, _lib.ptr(qkv), _lib.ptr(cos_t), _lib.ptr(sin_t), _lib.ptr(out),

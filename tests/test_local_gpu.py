@@ -70,3 +70,18 @@ def test_unsupported_shape_keeps_pytorch_path(device):
     y = layer.forward_chunk(x)
     layer.fused = False
     torch.testing.assert_close(y, layer.forward_chunk(x))
+
+
+def test_tables_built_under_inference_mode_serve_training(device):
+    """The rotary tables are cached per shape; the first use may be an
+    inference-mode prefill, and a later training step must still work."""
+    from exploration_amd import local
+
+    local._tables.clear()
+    layer = _block(64, 1, 16, device, torch.float32)
+    x = torch.randn(1, 40, 64, device=device)
+    with torch.inference_mode():
+        layer.forward_chunk(x)
+    xi = x.clone().requires_grad_()
+    layer.forward_chunk(xi).sum().backward()
+    assert xi.grad is not None and torch.isfinite(xi.grad).all()
