@@ -358,12 +358,13 @@ class StackModel(nn.Module):
     def embed(self, input_ids):
         """``self.embedding(ids)`` without the embedding's sort-based backward
         (a device sort and a look-back segment pass). Vocabularies up to 4096
-        (the byte-level configurations): a one-hot fp32 product, exactly the
-        weight rows forward and a fixed-order, deterministic product backward.
-        Larger ones: a row gather, whose backward adds rows with atomics."""
+        (the byte-level configurations) with at most 2^28 one-hot elements: a
+        one-hot fp32 product, exactly the weight rows forward and a
+        fixed-order, deterministic product backward. Otherwise: a row gather,
+        whose backward adds rows with atomics."""
         w = self.embedding.weight
         flat = input_ids.reshape(-1)
-        if w.shape[0] <= 4096:
+        if w.shape[0] <= 4096 and flat.numel() * w.shape[0] <= 1 << 28:
             with torch.autocast(w.device.type, enabled=False):
                 onehot = F.one_hot(flat, w.shape[0]).to(w.dtype)
                 x = onehot @ w
