@@ -258,27 +258,30 @@ __global__ __launch_bounds__(64) void halo_bwd_kernel(HaloArgs a) {
 //    key's K (and V) slice of 64 / LPK dims, every query (dO) row is a
 //    broadcast read, the LPK slice sums meet through cross-lane adds;
 //  * column phases (output, dq, dk, dv): lane = head-dim column d; the lane
-//    holds its column of V, K, Q or dO, the P / dS rows are broadcast reads.
-// The rotary transposes of dq and dk pair column d with d + 32 and go
-// through an LDS scratch tile.
-template <int B_>
+//    holds its column of V, K, Q or dO, the P / dS rows are broadcast reads,
+//    and the rotary transposes of dq and dk pair column d with lane d ^ 32.
+// The staged tiles keep the element type (the rotated rows are rounded to
+// it anyway): half the LDS of fp32 tiles, so more one-wave workgroups share
+// a CU and hide each other's memory waits.
+template <typename T, int B_>
 struct Halo64 {
   static constexpr int HD = 64, HALF = 32, W = 2 * B_, LPK = 64 / W, SL = HD / LPK;
-  static constexpr int LD = HD + 4, PS = W + 4;  // 16-byte aligned rows
-  static constexpr int NP = B_ * HALF / 64;
-  static_assert(LPK >= 1 && SL % 4 == 0 && W % 4 == 0, "shape");
+  static constexpr int E = Vec16<T>::n;          // elements per 16-byte read
+  static constexpr int LD = HD + E;              // element-type rows, 16-byte aligned
+  static constexpr int PS = W + 4;               // fp32 probability rows
+  static_assert(LPK >= 1 && SL % E == 0 && W % 4 == 0, "shape");
 };
 
-// Stage query block g (rotated), its window keys (rotated) and values, as
-// fp32. Every global load of the unit is issued before the first store
-// (16-byte vectors, clamped indices instead of predicates), so the wave waits
-// for one memory round trip, not one per element.
+// Stage query block g (rotated), its window keys (rotated) and values in the
+// element type. Every global load of the unit is issued before the first
+// store (16-byte vectors, clamped indices instead of predicates), so the
+// wave waits for one memory round trip, not one per element.
 template <typename T, int B_>
-__device__ __forceinline__ void stage64(const HaloArgs& a, const T* qkv, int64_t row0, int h, int g, float* qs,
-                                        float* ks, float* vs) {
-  typedef Halo64<B_> S;
+__device__ __forceinline__ void stage64(const HaloArgs& a, const T* qkv, int64_t row0, int h, int g, T* qs, T* ks,
+                                        T* vs) {
+  typedef Halo64<T, B_> S;
   typedef typename Vec16<T>::type V;
-  constexpr int E = Vec16<T>::n, VPR = S::HD / E, HV = VPR / 2, E4 = E / 4;
+  constexpr int E = S::E, VPR = S::HD / E, HV = VPR / 2, E4 = E / 4;
   constexpr int NQ = B_ * HV, NK = S::W * HV, NV = S::W * VPR;
   constexpr int TQ = (NQ + 63) / 64, TK = (NK + 63) / 64, TV = (NV + 63) / 64;
   const int lane = threadIdx.x;
@@ -317,42 +320,48 @@ __device__ __forceinline__ void stage64(const HaloArgs& a, const T* qkv, int64_t
   for (int t = 0; t < TQ; ++t) {
     const int e = lane + 64 * t, i = min(e, NQ - 1) / HV, c = e % HV;
     if (e >= NQ) break;
+    V lo_out, hi_out;
 #pragma unroll
     for (int u = 0; u < E; ++u) {
       const float lo = to_float<T>(ql[t][u]), hi = to_float<T>(qh[t][u]);
       const float cs = qc[t][u / 4][u % 4], sn = qn[t][u / 4][u % 4];
-      qs[i * S::LD + c * E + u] = round_to<T>(lo * cs - hi * sn);
-      qs[i * S::LD + c * E + u + S::HALF] = round_to<T>(hi * cs + lo * sn);
+      lo_out[u] = from_float<T>(lo * cs - hi * sn);
+      hi_out[u] = from_float<T>(hi * cs + lo * sn);
     }
+    *reinterpret_cast<V*>(qs + i * S::LD + c * E) = lo_out;
+    *reinterpret_cast<V*>(qs + i * S::LD + c * E + S::HALF) = hi_out;
   }
 #pragma unroll
   for (int t = 0; t < TK; ++t) {
     const int e = lane + 64 * t, kk = min(e, NK - 1) / HV, c = e % HV;
     if (e >= NK) break;
+    V lo_out, hi_out;
 #pragma unroll
     for (int u = 0; u < E; ++u) {
       const float lo = to_float<T>(kl[t][u]), hi = to_float<T>(kh[t][u]);
       const float cs = kc[t][u / 4][u % 4], sn = kn[t][u / 4][u % 4];
-      ks[kk * S::LD + c * E + u] = round_to<T>(lo * cs - hi * sn);
-      ks[kk * S::LD + c * E + u + S::HALF] = round_to<T>(hi * cs + lo * sn);
+      lo_out[u] = from_float<T>(lo * cs - hi * sn);
+      hi_out[u] = from_float<T>(hi * cs + lo * sn);
     }
+    *reinterpret_cast<V*>(ks + kk * S::LD + c * E) = lo_out;
+    *reinterpret_cast<V*>(ks + kk * S::LD + c * E + S::HALF) = hi_out;
   }
 #pragma unroll
   for (int t = 0; t < TV; ++t) {
     const int e = lane + 64 * t, kk = min(e, NV - 1) / VPR, c = e % VPR;
     if (e >= NV) break;
-#pragma unroll
-    for (int u = 0; u < E; ++u) vs[kk * S::LD + c * E + u] = to_float<T>(vv[t][u]);
+    *reinterpret_cast<V*>(vs + kk * S::LD + c * E) = vv[t];
   }
 }
 
-// dO and O rows of query block g as fp32 (zero beyond the n real rows), all
-// loads first.
+// dO rows of query block g in the element type (zero beyond the n real rows)
+// and delta = rowsum(dO * O) from the same loads (the VPR lanes of a row
+// reduce through cross-lane adds): O itself is never staged.
 template <typename T, int B_>
-__device__ __forceinline__ void stage_rows64(const HaloArgs& a, int bi, int h, int g, float* dos, float* os) {
-  typedef Halo64<B_> S;
+__device__ __forceinline__ void stage_rows64(const HaloArgs& a, int bi, int h, int g, T* dos, float* delta) {
+  typedef Halo64<T, B_> S;
   typedef typename Vec16<T>::type V;
-  constexpr int E = Vec16<T>::n, VPR = S::HD / E, N = B_ * VPR, TT = (N + 63) / 64;
+  constexpr int E = S::E, VPR = S::HD / E, N = B_ * VPR, TT = (N + 63) / 64;
   const int lane = threadIdx.x;
   const int64_t dim = (int64_t)a.H * S::HD;
   const T* dout = reinterpret_cast<const T*>(a.dout);
@@ -369,12 +378,20 @@ __device__ __forceinline__ void stage_rows64(const HaloArgs& a, int bi, int h, i
 #pragma unroll
   for (int t = 0; t < TT; ++t) {
     const int e = lane + 64 * t, i = min(e, N - 1) / VPR, c = e % VPR;
-    if (e >= N) break;
     const bool real = g * B_ + i < a.n;
+    float sd = 0.f;
 #pragma unroll
-    for (int u = 0; u < E; ++u) {
-      dos[i * S::LD + c * E + u] = real ? to_float<T>(gv[t][u]) : 0.f;
-      os[i * S::LD + c * E + u] = real ? to_float<T>(ov[t][u]) : 0.f;
+    for (int u = 0; u < E; ++u) sd += to_float<T>(gv[t][u]) * to_float<T>(ov[t][u]);
+#pragma unroll
+    for (int off = 1; off < VPR; off <<= 1) sd += __shfl_xor(sd, off, 64);  // every lane takes part
+    if (e < N) {  // N is a multiple of VPR: a row's lanes agree
+      if (!real) {
+        sd = 0.f;
+#pragma unroll
+        for (int u = 0; u < E; ++u) gv[t][u] = from_float<T>(0.f);
+      }
+      *reinterpret_cast<V*>(dos + i * S::LD + c * E) = gv[t];
+      if (c == 0) delta[i] = sd;
     }
   }
 }
@@ -387,6 +404,22 @@ __device__ __forceinline__ float slice_sum(float x) {
   return x;
 }
 
+// Dot of an element-type LDS row slice (broadcast reads) with fp32 registers.
+template <typename T, int N>
+__device__ __forceinline__ float dot_row(const T* row, const float (&reg)[N]) {
+  typedef typename Vec16<T>::type V;
+  constexpr int E = Vec16<T>::n;
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < N; c += E) {
+    const V v = *reinterpret_cast<const V*>(row + c);
+#pragma unroll
+    for (int u = 0; u < E; ++u) s += to_float<T>(v[u]) * reg[c + u];
+  }
+  return s;
+}
+
+// Dot of an fp32 LDS row (broadcast reads) with fp32 registers.
 template <int N>
 __device__ __forceinline__ float dot_bcast(const float* row, const float (&reg)[N]) {
   float s = 0.f;
@@ -399,16 +432,16 @@ __device__ __forceinline__ float dot_bcast(const float* row, const float (&reg)[
 }
 
 // Masked scores of query block g (row phase) and their row softmax, into ps.
-template <int B_>
-__device__ __forceinline__ void probs64(const HaloArgs& a, int g, const float* qs, const float (&kreg)[Halo64<B_>::SL],
-                                        float* ps) {
-  typedef Halo64<B_> S;
+template <typename T, int B_>
+__device__ __forceinline__ void probs64(const HaloArgs& a, int g, const T* qs,
+                                        const float (&kreg)[Halo64<T, B_>::SL], float* ps) {
+  typedef Halo64<T, B_> S;
   const int lane = threadIdx.x, kk = lane % S::W, sl = lane / S::W;
   const int64_t kp = a.start + (int64_t)(g - 1) * B_ + kk;
   const bool key_ok = kp >= a.first_key && kp < a.start + a.n;
 #pragma unroll 4
   for (int i = 0; i < B_; ++i) {
-    const float s = slice_sum<S::W>(dot_bcast(qs + i * S::LD + sl * S::SL, kreg));
+    const float s = slice_sum<S::W>(dot_row<T>(qs + i * S::LD + sl * S::SL, kreg));
     if (sl == 0) ps[i * S::PS + kk] = (key_ok && kk <= i + B_) ? s * a.scale : kNegInf;
   }
   __syncthreads();
@@ -440,10 +473,19 @@ __device__ __forceinline__ void probs64(const HaloArgs& a, int g, const float* q
   __syncthreads();
 }
 
+// The rotary transpose of a gradient column held as lane = d: the partner
+// column d ^ 32 comes from the lane d ^ 32.
+__device__ __forceinline__ float rotary_back(float dy, int d, const float* cos_row, const float* sin_row) {
+  const float other = __shfl_xor(dy, 32, 64);
+  const float c = cos_row[d & 31], s = sin_row[d & 31];
+  return d < 32 ? dy * c + other * s : dy * c - other * s;
+}
+
 template <typename T, int B_>
 __global__ __launch_bounds__(64) void halo_fwd64_kernel(HaloArgs a) {
-  typedef Halo64<B_> S;
-  __shared__ __attribute__((aligned(16))) float qs[B_ * S::LD], ks[S::W * S::LD], vs[S::W * S::LD], ps[B_ * S::PS];
+  typedef Halo64<T, B_> S;
+  __shared__ __attribute__((aligned(16))) T qs[B_ * S::LD], ks[S::W * S::LD], vs[S::W * S::LD];
+  __shared__ __attribute__((aligned(16))) float ps[B_ * S::PS];
   const int lane = threadIdx.x;
   const int h = (int)(blockIdx.x % (unsigned)a.H);
   const int g = (int)((blockIdx.x / (unsigned)a.H) % (unsigned)a.G);
@@ -455,12 +497,12 @@ __global__ __launch_bounds__(64) void halo_fwd64_kernel(HaloArgs a) {
   {
     const int kk = lane % S::W, sl = lane / S::W;
 #pragma unroll
-    for (int c = 0; c < S::SL; ++c) kreg[c] = ks[kk * S::LD + sl * S::SL + c];
+    for (int c = 0; c < S::SL; ++c) kreg[c] = to_float<T>(ks[kk * S::LD + sl * S::SL + c]);
   }
-  probs64<B_>(a, g, qs, kreg, ps);
+  probs64<T, B_>(a, g, qs, kreg, ps);
   float vcol[S::W];
 #pragma unroll
-  for (int kk = 0; kk < S::W; ++kk) vcol[kk] = vs[kk * S::LD + lane];
+  for (int kk = 0; kk < S::W; ++kk) vcol[kk] = to_float<T>(vs[kk * S::LD + lane]);
   T* out = reinterpret_cast<T*>(a.out);
   const int64_t dim = (int64_t)a.H * S::HD;
 #pragma unroll 4
@@ -473,9 +515,10 @@ __global__ __launch_bounds__(64) void halo_fwd64_kernel(HaloArgs a) {
 
 template <typename T, int B_>
 __global__ __launch_bounds__(64) void halo_bwd64_kernel(HaloArgs a) {
-  typedef Halo64<B_> S;
-  __shared__ __attribute__((aligned(16))) float qs[B_ * S::LD], ks[S::W * S::LD], vs[S::W * S::LD];
-  __shared__ __attribute__((aligned(16))) float dos[B_ * S::LD], scr[B_ * S::LD], ps[B_ * S::PS], dss[B_ * S::PS];
+  typedef Halo64<T, B_> S;
+  __shared__ __attribute__((aligned(16))) T qs[B_ * S::LD], ks[S::W * S::LD], vs[S::W * S::LD];
+  __shared__ __attribute__((aligned(16))) T dos[B_ * S::LD];
+  __shared__ __attribute__((aligned(16))) float ps[B_ * S::PS], dss[B_ * S::PS];
   __shared__ float delta[B_];
   const int lane = threadIdx.x;
   const int h = (int)(blockIdx.x % (unsigned)a.H);
@@ -486,117 +529,82 @@ __global__ __launch_bounds__(64) void halo_bwd64_kernel(HaloArgs a) {
   const T* qkv = reinterpret_cast<const T*>(a.qkv);
   T* dqkv = reinterpret_cast<T*>(a.dqkv);
   auto at = [&](int row, int slot, int d) { return ((row0 + row) * 3 + slot) * dim + (int64_t)h * S::HD + d; };
-  const int kk_l = lane % S::W, sl = lane / S::W;
+  const int kk_l = lane % S::W, sl = lane / S::W, d = lane;
 
-  float dk_lo[S::NP], dk_hi[S::NP], dv[B_];
+  // column d of dk and dv of block r's rows, summed over both roles
+  float dk[B_], dv[B_];
 #pragma unroll
-  for (int p = 0; p < S::NP; ++p) dk_lo[p] = dk_hi[p] = 0.f;
-#pragma unroll
-  for (int i = 0; i < B_; ++i) dv[i] = 0.f;
+  for (int i = 0; i < B_; ++i) dk[i] = dv[i] = 0.f;
 
   for (int role = 0; role < 2; ++role) {
     const int g = role == 0 ? r - 1 : r;  // role 0: own block of query block r-1; role 1: previous of query block r
     if (g < 0 || g >= a.G) continue;      // uniform over the wave
     __syncthreads();
     stage64<T, B_>(a, qkv, row0, h, g, qs, ks, vs);
-    // dO rows and delta = rowsum(dO * O) (O read once, into the scratch tile)
-    stage_rows64<T, B_>(a, bi, h, g, dos, scr);
+    stage_rows64<T, B_>(a, bi, h, g, dos, delta);
     __syncthreads();
     {
-      // delta = rowsum(dO * O): 64 / B_ adjacent lanes per row
-      constexpr int LR = 64 / B_, DL = S::HD / LR;
-      const int i = lane / LR, part = lane % LR;
-      float sd = 0.f;
+      float kreg[S::SL];
 #pragma unroll
-      for (int c = 0; c < DL; c += 4) {
-        const f32x4 x = *reinterpret_cast<const f32x4*>(dos + i * S::LD + part * DL + c);
-        const f32x4 y = *reinterpret_cast<const f32x4*>(scr + i * S::LD + part * DL + c);
-        sd += x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
-      }
-#pragma unroll
-      for (int off = 1; off < LR; off <<= 1) sd += __shfl_xor(sd, off, 64);
-      if (part == 0) delta[i] = sd;
+      for (int c = 0; c < S::SL; ++c) kreg[c] = to_float<T>(ks[kk_l * S::LD + sl * S::SL + c]);
+      probs64<T, B_>(a, g, qs, kreg, ps);
     }
-    float kreg[S::SL], vreg[S::SL];
+    float vreg[S::SL];
 #pragma unroll
-    for (int c = 0; c < S::SL; ++c) {
-      kreg[c] = ks[kk_l * S::LD + sl * S::SL + c];
-      vreg[c] = vs[kk_l * S::LD + sl * S::SL + c];
-    }
-    probs64<B_>(a, g, qs, kreg, ps);  // (its barriers also publish delta)
+    for (int c = 0; c < S::SL; ++c) vreg[c] = to_float<T>(vs[kk_l * S::LD + sl * S::SL + c]);
     // dS = P (dP - delta) with dP = dO V^T (row phase)
-#pragma unroll 4
+#pragma unroll 2
     for (int i = 0; i < B_; ++i) {
-      const float dp = slice_sum<S::W>(dot_bcast(dos + i * S::LD + sl * S::SL, vreg));
-      if (sl == 0) {
-        const float pv = ps[i * S::PS + kk_l];
-        dss[i * S::PS + kk_l] = pv * (dp - delta[i]);
-      }
+      const float dp = slice_sum<S::W>(dot_row<T>(dos + i * S::LD + sl * S::SL, vreg));
+      if (sl == 0) dss[i * S::PS + kk_l] = ps[i * S::PS + kk_l] * (dp - delta[i]);
     }
     __syncthreads();
     // column phase, lane = d
-    const int d = lane;
     if (role == 0) {
+      // dq of block r = scale * dS K, transposed through the query rotary
       float kcol[S::W];
 #pragma unroll
-      for (int kk = 0; kk < S::W; ++kk) kcol[kk] = ks[kk * S::LD + d];
+      for (int kk = 0; kk < S::W; ++kk) kcol[kk] = to_float<T>(ks[kk * S::LD + d]);
 #pragma unroll 4
-      for (int i = 0; i < B_; ++i) scr[i * S::LD + d] = a.scale * dot_bcast(dss + i * S::PS, kcol);
-    }
-    const int kk0 = role == 0 ? B_ : 0;
-    float qcol[B_], docol[B_];
-#pragma unroll
-    for (int i = 0; i < B_; ++i) {
-      qcol[i] = qs[i * S::LD + d];
-      docol[i] = dos[i * S::LD + d];
-    }
-    // dv of this role's window rows; dk (before its rotary) into ks rows
-    // kk0.. (the keys are no longer read in this role)
-    __syncthreads();
-#pragma unroll
-    for (int i2 = 0; i2 < B_; ++i2) {
-      const int kk = kk0 + i2;
-      float sv = 0.f, sk = 0.f;
-#pragma unroll
       for (int i = 0; i < B_; ++i) {
-        sv += ps[i * S::PS + kk] * docol[i];
-        sk += dss[i * S::PS + kk] * qcol[i];
+        const float dy = a.scale * dot_bcast(dss + i * S::PS, kcol);
+        const float dx = rotary_back(dy, d, a.cos_t + (B_ + i) * S::HALF, a.sin_t + (B_ + i) * S::HALF);
+        dqkv[at(r * B_ + i, 0, d)] = from_float<T>(dx);
       }
-      dv[i2] += sv;
-      ks[kk * S::LD + d] = a.scale * sk;
     }
-    __syncthreads();
-    if (role == 0) {
-      for (int e = lane; e < B_ * S::HALF; e += 64) {
-        const int i = e / S::HALF, j = e % S::HALF;
-        const float lo = scr[i * S::LD + j], hi = scr[i * S::LD + j + S::HALF];
-        const float c = a.cos_t[(B_ + i) * S::HALF + j], s = a.sin_t[(B_ + i) * S::HALF + j];
-        dqkv[at(r * B_ + i, 0, j)] = from_float<T>(lo * c + hi * s);
-        dqkv[at(r * B_ + i, 0, j + S::HALF)] = from_float<T>(hi * c - lo * s);
+    // this role's window rows kk0 + i2 are block r's rows i2; dv and the
+    // unrotated dk take P / dS rows as 16-byte broadcasts
+    const int kk0 = role == 0 ? B_ : 0;
+    float sk[B_];
+#pragma unroll
+    for (int i2 = 0; i2 < B_; ++i2) sk[i2] = 0.f;
+#pragma unroll 2
+    for (int i = 0; i < B_; ++i) {
+      const float qv = to_float<T>(qs[i * S::LD + d]), gv = to_float<T>(dos[i * S::LD + d]);
+#pragma unroll
+      for (int i2 = 0; i2 < B_; i2 += 4) {
+        const f32x4 p4 = *reinterpret_cast<const f32x4*>(ps + i * S::PS + kk0 + i2);
+        const f32x4 s4 = *reinterpret_cast<const f32x4*>(dss + i * S::PS + kk0 + i2);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          dv[i2 + u] += p4[u] * gv;
+          sk[i2 + u] += s4[u] * qv;
+        }
       }
     }
 #pragma unroll
-    for (int p = 0; p < S::NP; ++p) {
-      const int e = lane + 64 * p;
-      const int i2 = e / S::HALF, j = e % S::HALF, kk = kk0 + i2;
-      const float lo = ks[kk * S::LD + j], hi = ks[kk * S::LD + j + S::HALF];
-      const float c = a.cos_t[kk * S::HALF + j], s = a.sin_t[kk * S::HALF + j];
-      dk_lo[p] += lo * c + hi * s;
-      dk_hi[p] += hi * c - lo * s;
-    }
+    for (int i2 = 0; i2 < B_; ++i2)
+      dk[i2] += rotary_back(a.scale * sk[i2], d, a.cos_t + (kk0 + i2) * S::HALF, a.sin_t + (kk0 + i2) * S::HALF);
   }
   if (r == 0) {
-    for (int e = lane; e < B_ * S::HD; e += 64) dqkv[at(e / S::HD, 0, e % S::HD)] = from_float<T>(0.f);
+#pragma unroll
+    for (int i = 0; i < B_; ++i) dqkv[at(i, 0, d)] = from_float<T>(0.f);
   }
 #pragma unroll
-  for (int p = 0; p < S::NP; ++p) {
-    const int e = lane + 64 * p;
-    const int i2 = e / S::HALF, j = e % S::HALF;
-    dqkv[at(r * B_ + i2, 1, j)] = from_float<T>(dk_lo[p]);
-    dqkv[at(r * B_ + i2, 1, j + S::HALF)] = from_float<T>(dk_hi[p]);
+  for (int i2 = 0; i2 < B_; ++i2) {
+    dqkv[at(r * B_ + i2, 1, d)] = from_float<T>(dk[i2]);
+    dqkv[at(r * B_ + i2, 2, d)] = from_float<T>(dv[i2]);
   }
-#pragma unroll
-  for (int i2 = 0; i2 < B_; ++i2) dqkv[at(r * B_ + i2, 2, lane)] = from_float<T>(dv[i2]);
 }
 
 template <int B_, int HD>
