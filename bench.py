@@ -37,6 +37,9 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-model", action="store_true", help="skip the cfg5 Stack model training step")
     p.add_argument("--model-steps", type=int, default=20, help="timed cfg5 training steps")
+    p.add_argument("--dense-rows", choices=("causal", "last"), default="causal",
+                   help="diagnostic: 'last' puts every cfg2 query at the last position (all keys visible, "
+                        "no causal structure, twice the work); the headline uses 'causal'")
     return p.parse_args()
 
 
@@ -83,6 +86,8 @@ def bench_dense(args, torch, device):
     from exploration_amd.workloads import CFG2, dense_config, dense_flops, dense_forward_flops
 
     q, k, v, pos, do, b = dense_config(CFG2, device=device)
+    if args.dense_rows == "last":
+        pos = torch.full_like(pos, k.shape[1] - 1)
     q, k, v = (t.requires_grad_() for t in (q, k, v))
     flops = dense_flops(pos, k.shape[1], q.shape[2], q.shape[3])
     fwd_flops = dense_forward_flops(pos, k.shape[1], q.shape[2], q.shape[3])
@@ -303,7 +308,9 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "cfg2: dense gated attention forward+backward, bf16, B1 H8 N=Q=4096 D128 "
-                               "block 128, causal, q/k/v ~ N(0,1)/sqrt(128), dO ~ N(0,1)",
+                               "block 128, " + ("causal" if args.dense_rows == "causal" else
+                                                "every query at position 4095 (diagnostic)")
+                               + ", q/k/v ~ N(0,1)/sqrt(128), dO ~ N(0,1)",
                    "global_batch": 1, "seq_len": 4096, "heads": 8, "head_dim": 128, "block_size": 128,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": "dense forward+backward, one step (dense_fwd_fast, "
