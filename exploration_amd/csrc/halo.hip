@@ -607,6 +607,365 @@ __global__ __launch_bounds__(64) void halo_bwd64_kernel(HaloArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// b = 16, head_dim 64, 16-bit elements: the five products on MFMA
+// (v_mfma_f32_16x16x32: lane l holds A[l%16][8(l/16)+s], B[8(l/16)+s][l%16]
+// and C[4(l/16)+r][l%16]). Scores are computed transposed, S^T = K Q^T, so
+// lane l owns query row l%16 and keys 16t + 4(l/16) + r (t = 0, 1; r = 0..3):
+// row reductions are in-lane plus two exchanges (lanes l ^ 16, l ^ 32). The
+// same registers, packed in that key order, are the A operand of P V and
+// dS K; their B operand reads V and K from transposed LDS copies in the same
+// permuted key order (slot 8(l/16)+s holds key 4(l/16)+s for s < 4 and
+// 16+4(l/16)+s-4 for s >= 4). dK and dV contract over the block's 16 query
+// rows: the k slots 16..31 (lanes 32..63) are zero.
+struct HaloMfma {
+  static constexpr int B_ = 16, W = 32, HD = 64, HALF = 32;
+  static constexpr int LD = HD + 8;  // row-major 16-bit tiles (144-byte rows)
+  static constexpr int LK = W + 8;   // transposed K / V: [d][key]
+  static constexpr int LR = B_ + 8;  // transposed Q / dO: [d][row]; P^T, dS^T: [key][row]
+};
+
+template <typename T>
+using Vec4 = T __attribute__((ext_vector_type(4)));
+
+// Query block g rotated (rows; transposed too for the backward), its window
+// keys rotated (rows; transposed for the backward), values (rows for the
+// backward, transposed for the forward). Every global load first.
+template <typename T, bool BWD>
+__device__ __forceinline__ void stage_mfma(const HaloArgs& a, const T* qkv, int64_t row0, int h, int g, T* qs,
+                                           T* qts, T* ks, T* kts, T* vs, T* vts) {
+  typedef HaloMfma S;
+  typedef typename Vec16<T>::type V;
+  constexpr int E = 8, VPR = S::HD / E, HV = VPR / 2;
+  constexpr int TK = S::W * HV / 64, TV = S::W * VPR / 64;  // 2, 4 (the query block: one per lane)
+  const int lane = threadIdx.x;
+  const int64_t dim = (int64_t)a.H * S::HD;
+  auto src = [&](int r, int slot, int d) { return qkv + ((row0 + r) * 3 + slot) * dim + (int64_t)h * S::HD + d; };
+  const int qi = lane / HV, qc = lane % HV;
+  const V ql = load_vec<V>(src((g + 1) * S::B_ + qi, 0, qc * E));
+  const V qh = load_vec<V>(src((g + 1) * S::B_ + qi, 0, qc * E + S::HALF));
+  f32x4 qcs[2], qsn[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    qcs[u] = load_vec<f32x4>(a.cos_t + (S::B_ + qi) * S::HALF + qc * E + 4 * u);
+    qsn[u] = load_vec<f32x4>(a.sin_t + (S::B_ + qi) * S::HALF + qc * E + 4 * u);
+  }
+  V kl[TK], kh[TK], vv[TV];
+  f32x4 kcs[TK][2], ksn[TK][2];
+#pragma unroll
+  for (int t = 0; t < TK; ++t) {
+    const int e = lane + 64 * t, kk = e / HV, c = e % HV;
+    kl[t] = load_vec<V>(src(g * S::B_ + kk, 1, c * E));
+    kh[t] = load_vec<V>(src(g * S::B_ + kk, 1, c * E + S::HALF));
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      kcs[t][u] = load_vec<f32x4>(a.cos_t + kk * S::HALF + c * E + 4 * u);
+      ksn[t][u] = load_vec<f32x4>(a.sin_t + kk * S::HALF + c * E + 4 * u);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TV; ++t) {
+    const int e = lane + 64 * t, kk = e / VPR, c = e % VPR;
+    vv[t] = load_vec<V>(src(g * S::B_ + kk, 2, c * E));
+  }
+  // rotate a (lo, hi) pair of 8-element chunks; store rows and, if asked, columns
+  auto put = [&](const V& lo, const V& hi, const f32x4 (&cs)[2], const f32x4 (&sn)[2], int row, int c, T* rows,
+                 T* cols, int ldc) {
+    V lo_out, hi_out;
+#pragma unroll
+    for (int u = 0; u < E; ++u) {
+      const float x = to_float<T>(lo[u]), y = to_float<T>(hi[u]);
+      const float cu = cs[u / 4][u % 4], su = sn[u / 4][u % 4];
+      lo_out[u] = from_float<T>(x * cu - y * su);
+      hi_out[u] = from_float<T>(y * cu + x * su);
+    }
+    *reinterpret_cast<V*>(rows + row * S::LD + c * E) = lo_out;
+    *reinterpret_cast<V*>(rows + row * S::LD + c * E + S::HALF) = hi_out;
+    if (cols) {
+#pragma unroll
+      for (int u = 0; u < E; ++u) {
+        cols[(c * E + u) * ldc + row] = lo_out[u];
+        cols[(c * E + u + S::HALF) * ldc + row] = hi_out[u];
+      }
+    }
+  };
+  put(ql, qh, qcs, qsn, qi, qc, qs, BWD ? qts : nullptr, S::LR);
+#pragma unroll
+  for (int t = 0; t < TK; ++t) {
+    const int e = lane + 64 * t;
+    put(kl[t], kh[t], kcs[t], ksn[t], e / HV, e % HV, ks, BWD ? kts : nullptr, S::LK);
+  }
+#pragma unroll
+  for (int t = 0; t < TV; ++t) {
+    const int e = lane + 64 * t, kk = e / VPR, c = e % VPR;
+    if (BWD) {
+      *reinterpret_cast<V*>(vs + kk * S::LD + c * E) = vv[t];
+    } else {
+#pragma unroll
+      for (int u = 0; u < E; ++u) vts[(c * E + u) * S::LK + kk] = vv[t][u];
+    }
+  }
+}
+
+// dO rows of query block g (zero beyond the n real rows) as rows and
+// columns, and delta = rowsum(dO * O) from the same loads.
+template <typename T>
+__device__ __forceinline__ void stage_do_mfma(const HaloArgs& a, int bi, int h, int g, T* dos, T* dots,
+                                              float* delta) {
+  typedef HaloMfma S;
+  typedef typename Vec16<T>::type V;
+  constexpr int E = 8, VPR = S::HD / E, TT = S::B_ * VPR / 64;  // 2
+  const int lane = threadIdx.x;
+  const int64_t dim = (int64_t)a.H * S::HD;
+  const T* dout = reinterpret_cast<const T*>(a.dout);
+  const T* out = reinterpret_cast<const T*>(a.out);
+  V gv[TT], ov[TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    const int e = lane + 64 * t, i = e / VPR, c = e % VPR;
+    const int row = min(g * S::B_ + i, a.n - 1);
+    const int64_t o = ((int64_t)bi * a.n + row) * dim + (int64_t)h * S::HD + c * E;
+    gv[t] = load_vec<V>(dout + o);
+    ov[t] = load_vec<V>(out + o);
+  }
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    const int e = lane + 64 * t, i = e / VPR, c = e % VPR;
+    float sd = 0.f;
+#pragma unroll
+    for (int u = 0; u < E; ++u) sd += to_float<T>(gv[t][u]) * to_float<T>(ov[t][u]);
+#pragma unroll
+    for (int off = 1; off < VPR; off <<= 1) sd += __shfl_xor(sd, off, 64);
+    if (g * S::B_ + i >= a.n) {
+      sd = 0.f;
+#pragma unroll
+      for (int u = 0; u < E; ++u) gv[t][u] = from_float<T>(0.f);
+    }
+    *reinterpret_cast<V*>(dos + i * S::LD + c * E) = gv[t];
+#pragma unroll
+    for (int u = 0; u < E; ++u) dots[(c * E + u) * S::LR + i] = gv[t][u];
+    if (c == 0) delta[i] = sd;
+  }
+}
+
+// Transposed score-shaped tiles: c[t][r] = sum_d A[16t + 4(l/16) + r][d] * B[l%16][d]
+// with A = the row-major window tile (keys) and B the row-major query-block
+// tile: S^T from (K, Q), dP^T from (V, dO).
+template <typename T>
+__device__ __forceinline__ void window_tiles(const T* as, const T* bs, f32x4 (&c)[2]) {
+  typedef HaloMfma S;
+  typedef Mma16<T> M;
+  typedef typename M::Frag F;
+  const int lane = threadIdx.x, col = lane & 15, grp = lane >> 4;
+  const F b0 = *reinterpret_cast<const F*>(bs + col * S::LD + 8 * grp);
+  const F b1 = *reinterpret_cast<const F*>(bs + col * S::LD + 32 + 8 * grp);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const F a0 = *reinterpret_cast<const F*>(as + (16 * t + col) * S::LD + 8 * grp);
+    const F a1 = *reinterpret_cast<const F*>(as + (16 * t + col) * S::LD + 32 + 8 * grp);
+    c[t] = M::mma(a1, b1, M::mma(a0, b0, f32x4{0.f, 0.f, 0.f, 0.f}));
+  }
+}
+
+// Mask, scale and softmax of query row l%16 of block g; s holds S^T tiles in,
+// probabilities out.
+__device__ __forceinline__ void window_softmax(const HaloArgs& a, int g, f32x4 (&s)[2]) {
+  typedef HaloMfma S;
+  const int lane = threadIdx.x, i = lane & 15, grp = lane >> 4;
+  float m = kNegInf;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int kk = 16 * t + 4 * grp + r;
+      const int64_t kp = a.start + (int64_t)(g - 1) * S::B_ + kk;
+      const bool ok = kp >= a.first_key && kp < a.start + a.n && kk <= i + S::B_;
+      s[t][r] = ok ? s[t][r] * a.scale : kNegInf;
+      m = fmaxf(m, s[t][r]);
+    }
+  }
+  m = fmaxf(m, __shfl_xor(m, 16, 64));
+  m = fmaxf(m, __shfl_xor(m, 32, 64));
+  float sum = 0.f;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      s[t][r] = m == kNegInf ? 0.f : __expf(s[t][r] - m);
+      sum += s[t][r];
+    }
+  }
+  sum += __shfl_xor(sum, 16, 64);
+  sum += __shfl_xor(sum, 32, 64);
+  const float inv = sum > 0.f ? 1.f / sum : 0.f;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) s[t] *= inv;
+}
+
+// A operand (row l%16, key slots 8(l/16)..+7 in the permuted order) from the
+// lane's own score-shaped registers.
+template <typename T>
+__device__ __forceinline__ typename Mma16<T>::Frag pack_rows(const f32x4 (&x)[2]) {
+  typename Mma16<T>::Frag f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    f[u] = from_float<T>(x[0][u]);
+    f[u + 4] = from_float<T>(x[1][u]);
+  }
+  return f;
+}
+
+// B operand (key slots in the permuted order, column d) from a transposed
+// [d][key] tile.
+template <typename T>
+__device__ __forceinline__ typename Mma16<T>::Frag frag_keys(const T* ts, int d, int grp) {
+  const Vec4<T> lo = *reinterpret_cast<const Vec4<T>*>(ts + d * HaloMfma::LK + 4 * grp);
+  const Vec4<T> hi = *reinterpret_cast<const Vec4<T>*>(ts + d * HaloMfma::LK + 16 + 4 * grp);
+  typename Mma16<T>::Frag f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    f[u] = lo[u];
+    f[u + 4] = hi[u];
+  }
+  return f;
+}
+
+template <typename T>
+__global__ __launch_bounds__(64) void halo_fwd_mfma_kernel(HaloArgs a) {
+  typedef HaloMfma S;
+  typedef Mma16<T> M;
+  __shared__ __attribute__((aligned(16))) T qs[S::B_ * S::LD], ks[S::W * S::LD], vts[S::HD * S::LK];
+  const int lane = threadIdx.x, col = lane & 15, grp = lane >> 4;
+  const int h = (int)(blockIdx.x % (unsigned)a.H);
+  const int g = (int)((blockIdx.x / (unsigned)a.H) % (unsigned)a.G);
+  const int bi = (int)(blockIdx.x / ((unsigned)a.H * (unsigned)a.G));
+  const int64_t row0 = (int64_t)bi * (a.G + 1) * S::B_;
+  stage_mfma<T, false>(a, reinterpret_cast<const T*>(a.qkv), row0, h, g, qs, nullptr, ks, nullptr, nullptr, vts);
+  __syncthreads();
+  f32x4 p[2];
+  window_tiles<T>(ks, qs, p);
+  window_softmax(a, g, p);
+  const typename M::Frag pa = pack_rows<T>(p);
+  T* out = reinterpret_cast<T*>(a.out);
+  const int64_t dim = (int64_t)a.H * S::HD;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    const f32x4 o = M::mma(pa, frag_keys<T>(vts, 16 * dt + col, grp), f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = g * S::B_ + 4 * grp + r;
+      if (t < a.n) out[((int64_t)bi * a.n + t) * dim + (int64_t)h * S::HD + 16 * dt + col] = from_float<T>(o[r]);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(64) void halo_bwd_mfma_kernel(HaloArgs a) {
+  typedef HaloMfma S;
+  typedef Mma16<T> M;
+  typedef typename M::Frag F;
+  __shared__ __attribute__((aligned(16))) T qs[S::B_ * S::LD], ks[S::W * S::LD], vs[S::W * S::LD];
+  __shared__ __attribute__((aligned(16))) T dos[S::B_ * S::LD];
+  __shared__ __attribute__((aligned(16))) T qts[S::HD * S::LR], kts[S::HD * S::LK], dots[S::HD * S::LR];
+  __shared__ __attribute__((aligned(16))) T pts[S::B_ * S::LR], dsts[S::B_ * S::LR];
+  __shared__ float delta[S::B_];
+  const int lane = threadIdx.x, col = lane & 15, grp = lane >> 4;
+  const int h = (int)(blockIdx.x % (unsigned)a.H);
+  const int r = (int)((blockIdx.x / (unsigned)a.H) % (unsigned)(a.G + 1));
+  const int bi = (int)(blockIdx.x / ((unsigned)a.H * (unsigned)(a.G + 1)));
+  const int64_t row0 = (int64_t)bi * (a.G + 1) * S::B_;
+  const int64_t dim = (int64_t)a.H * S::HD;
+  const T* qkv = reinterpret_cast<const T*>(a.qkv);
+  T* dqkv = reinterpret_cast<T*>(a.dqkv);
+  auto at = [&](int row, int slot, int d) { return ((row0 + row) * 3 + slot) * dim + (int64_t)h * S::HD + d; };
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  F fzero;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) fzero[u] = from_float<T>(0.f);
+
+  // rows 4(l/16) + i of block r, columns 16 dt + l%16: dv, and dk after the
+  // rotary transpose, summed over both roles
+  f32x4 dk[4], dv[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) dk[dt] = dv[dt] = zero;
+
+#pragma unroll 1
+  for (int role = 0; role < 2; ++role) {
+    const int g = role == 0 ? r - 1 : r;  // role 0: own block of query block r-1; role 1: previous of query block r
+    if (g < 0 || g >= a.G) continue;      // uniform over the wave
+    __syncthreads();
+    stage_mfma<T, true>(a, qkv, row0, h, g, qs, qts, ks, kts, vs, nullptr);
+    stage_do_mfma<T>(a, bi, h, g, dos, dots, delta);
+    __syncthreads();
+    f32x4 p[2], ds[2];
+    window_tiles<T>(ks, qs, p);
+    window_softmax(a, g, p);
+    window_tiles<T>(vs, dos, ds);  // dP^T
+    const float dl = delta[col];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) ds[t] = p[t] * (ds[t] - dl);
+    if (role == 0) {
+      // dq of block r = scale dS K, through the query rotary transpose
+      const F da = pack_rows<T>(ds);
+      f32x4 y[4];
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) y[dt] = M::mma(da, frag_keys<T>(kts, 16 * dt + col, grp), zero);
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = 4 * grp + i, d = 16 * dt + col;
+          const float cs = a.cos_t[(S::B_ + row) * S::HALF + d], sn = a.sin_t[(S::B_ + row) * S::HALF + d];
+          const float lo = a.scale * y[dt][i], hi = a.scale * y[dt + 2][i];
+          dqkv[at(r * S::B_ + row, 0, d)] = from_float<T>(lo * cs + hi * sn);
+          dqkv[at(r * S::B_ + row, 0, d + S::HALF)] = from_float<T>(hi * cs - lo * sn);
+        }
+      }
+    }
+    // this role's window keys kk0 + j are block r's rows j
+    const int th = role == 0 ? 1 : 0, kk0 = 16 * th;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pts[(4 * grp + i) * S::LR + col] = from_float<T>(p[th][i]);
+      dsts[(4 * grp + i) * S::LR + col] = from_float<T>(ds[th][i]);
+    }
+    __syncthreads();
+    const bool kin = grp < 2;  // k slots 0..15: the 16 query rows
+    const F pa = kin ? *reinterpret_cast<const F*>(pts + col * S::LR + 8 * grp) : fzero;
+    const F sa = kin ? *reinterpret_cast<const F*>(dsts + col * S::LR + 8 * grp) : fzero;
+    f32x4 kt[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const int d = 16 * dt + col;
+      const F ob = kin ? *reinterpret_cast<const F*>(dots + d * S::LR + 8 * grp) : fzero;
+      const F qb = kin ? *reinterpret_cast<const F*>(qts + d * S::LR + 8 * grp) : fzero;
+      dv[dt] = M::mma(pa, ob, dv[dt]);
+      kt[dt] = M::mma(sa, qb, zero);
+    }
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kk = kk0 + 4 * grp + i, d = 16 * dt + col;
+        const float cs = a.cos_t[kk * S::HALF + d], sn = a.sin_t[kk * S::HALF + d];
+        const float lo = a.scale * kt[dt][i], hi = a.scale * kt[dt + 2][i];
+        dk[dt][i] += lo * cs + hi * sn;
+        dk[dt + 2][i] += hi * cs - lo * sn;
+      }
+    }
+  }
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = r * S::B_ + 4 * grp + i, d = 16 * dt + col;
+      if (r == 0) dqkv[at(row, 0, d)] = from_float<T>(0.f);
+      dqkv[at(row, 1, d)] = from_float<T>(dk[dt][i]);
+      dqkv[at(row, 2, d)] = from_float<T>(dv[dt][i]);
+    }
+  }
+}
+
 template <int B_, int HD>
 constexpr size_t bwd_lds() {
   typedef HaloShape<B_, HD> S;
@@ -619,7 +978,10 @@ template <typename T, bool BWD>
 hipError_t dispatch(const HaloArgs& a, hipStream_t s) {
   const unsigned units = (unsigned)((int64_t)a.B * (BWD ? a.G + 1 : a.G) * a.H);
   auto go = [&]<int B_, int HD>() {
-    if constexpr (HD == 64) {
+    if constexpr (HD == 64 && B_ == 16 && sizeof(T) == 2) {
+      if constexpr (BWD) hipLaunchKernelGGL((halo_bwd_mfma_kernel<T>), dim3(units), dim3(64), 0, s, a);
+      else hipLaunchKernelGGL((halo_fwd_mfma_kernel<T>), dim3(units), dim3(64), 0, s, a);
+    } else if constexpr (HD == 64) {
       if constexpr (BWD) hipLaunchKernelGGL((halo_bwd64_kernel<T, B_>), dim3(units), dim3(64), 0, s, a);
       else hipLaunchKernelGGL((halo_fwd64_kernel<T, B_>), dim3(units), dim3(64), 0, s, a);
     } else {
