@@ -23,8 +23,6 @@ struct HaloArgs {
   void* dqkv;             // [B, (G+1)*b, 3, H, hd]
 };
 
-// LDS bytes the backward needs (0 if the shape is outside the kernels).
-size_t halo_lds_bytes(int b, int hd);
 bool halo_supported(int b, int hd);
 hipError_t launch_halo_fwd(int dtype, const HaloArgs& a, hipStream_t stream);
 hipError_t launch_halo_bwd(int dtype, const HaloArgs& a, hipStream_t stream);

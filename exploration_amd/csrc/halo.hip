@@ -966,12 +966,6 @@ __global__ __launch_bounds__(64) void halo_bwd_mfma_kernel(HaloArgs a) {
   }
 }
 
-template <int B_, int HD>
-constexpr size_t bwd_lds() {
-  typedef HaloShape<B_, HD> S;
-  return sizeof(float) * (7 * B_ * S::LD + 2 * B_ * S::PS + B_);
-}
-
 // Instantiated shapes: the reference configurations use b = 16 (head_dim 64
 // at stack_100m); every (b, hd) below fits the backward's LDS in 64 KiB.
 template <typename T, bool BWD>
@@ -1017,13 +1011,6 @@ hipError_t launch(int dtype, bool bwd, const HaloArgs& a, hipStream_t s) {
 
 bool halo_supported(int b, int hd) {
   return ((b == 4 || b == 8 || b == 16) && (hd == 32 || hd == 64 || hd == 128)) || (b == 32 && hd == 32);
-}
-
-size_t halo_lds_bytes(int b, int hd) {
-  if (!halo_supported(b, hd)) return 0;
-  if (b == 32) return bwd_lds<32, 32>();
-  const int w = 2 * b;
-  return sizeof(float) * (7 * b * (hd + 1) + 2 * b * (w + 1) + b);
 }
 
 hipError_t launch_halo_fwd(int dtype, const HaloArgs& a, hipStream_t stream) { return launch(dtype, false, a, stream); }
