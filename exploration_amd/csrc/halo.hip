@@ -628,46 +628,76 @@ struct HaloMfma {
 template <typename T>
 using Vec4 = T __attribute__((ext_vector_type(4)));
 
-// Query block g rotated (rows; transposed too for the backward), its window
-// keys rotated (rows; transposed for the backward), values (rows for the
-// backward, transposed for the forward). Every global load first.
+// The global loads of one unit (query block g of batch row bi, head h): the
+// query block, its window keys and values, their rotary cos/sin, and for the
+// backward the block's dO and O rows. Loading and storing are separate so
+// the backward can have the next unit's loads in flight during the products.
+template <typename T>
+struct HaloLoads {
+  typedef typename Vec16<T>::type V;
+  V ql, qh, kl[2], kh[2], vv[4], gv[2], ov[2];
+  f32x4 qcs[2], qsn[2], kcs[2][2], ksn[2][2];
+};
+
 template <typename T, bool BWD>
-__device__ __forceinline__ void stage_mfma(const HaloArgs& a, const T* qkv, int64_t row0, int h, int g, T* qs,
-                                           T* qts, T* ks, T* kts, T* vs, T* vts) {
+__device__ __forceinline__ void load_unit(const HaloArgs& a, int64_t row0, int bi, int h, int g, HaloLoads<T>& L) {
   typedef HaloMfma S;
   typedef typename Vec16<T>::type V;
   constexpr int E = 8, VPR = S::HD / E, HV = VPR / 2;
-  constexpr int TK = S::W * HV / 64, TV = S::W * VPR / 64;  // 2, 4 (the query block: one per lane)
   const int lane = threadIdx.x;
   const int64_t dim = (int64_t)a.H * S::HD;
+  const T* qkv = reinterpret_cast<const T*>(a.qkv);
   auto src = [&](int r, int slot, int d) { return qkv + ((row0 + r) * 3 + slot) * dim + (int64_t)h * S::HD + d; };
   const int qi = lane / HV, qc = lane % HV;
-  const V ql = load_vec<V>(src((g + 1) * S::B_ + qi, 0, qc * E));
-  const V qh = load_vec<V>(src((g + 1) * S::B_ + qi, 0, qc * E + S::HALF));
-  f32x4 qcs[2], qsn[2];
+  L.ql = load_vec<V>(src((g + 1) * S::B_ + qi, 0, qc * E));
+  L.qh = load_vec<V>(src((g + 1) * S::B_ + qi, 0, qc * E + S::HALF));
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
-    qcs[u] = load_vec<f32x4>(a.cos_t + (S::B_ + qi) * S::HALF + qc * E + 4 * u);
-    qsn[u] = load_vec<f32x4>(a.sin_t + (S::B_ + qi) * S::HALF + qc * E + 4 * u);
+    L.qcs[u] = load_vec<f32x4>(a.cos_t + (S::B_ + qi) * S::HALF + qc * E + 4 * u);
+    L.qsn[u] = load_vec<f32x4>(a.sin_t + (S::B_ + qi) * S::HALF + qc * E + 4 * u);
   }
-  V kl[TK], kh[TK], vv[TV];
-  f32x4 kcs[TK][2], ksn[TK][2];
 #pragma unroll
-  for (int t = 0; t < TK; ++t) {
+  for (int t = 0; t < 2; ++t) {
     const int e = lane + 64 * t, kk = e / HV, c = e % HV;
-    kl[t] = load_vec<V>(src(g * S::B_ + kk, 1, c * E));
-    kh[t] = load_vec<V>(src(g * S::B_ + kk, 1, c * E + S::HALF));
+    L.kl[t] = load_vec<V>(src(g * S::B_ + kk, 1, c * E));
+    L.kh[t] = load_vec<V>(src(g * S::B_ + kk, 1, c * E + S::HALF));
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      kcs[t][u] = load_vec<f32x4>(a.cos_t + kk * S::HALF + c * E + 4 * u);
-      ksn[t][u] = load_vec<f32x4>(a.sin_t + kk * S::HALF + c * E + 4 * u);
+      L.kcs[t][u] = load_vec<f32x4>(a.cos_t + kk * S::HALF + c * E + 4 * u);
+      L.ksn[t][u] = load_vec<f32x4>(a.sin_t + kk * S::HALF + c * E + 4 * u);
     }
   }
 #pragma unroll
-  for (int t = 0; t < TV; ++t) {
+  for (int t = 0; t < 4; ++t) {
     const int e = lane + 64 * t, kk = e / VPR, c = e % VPR;
-    vv[t] = load_vec<V>(src(g * S::B_ + kk, 2, c * E));
+    L.vv[t] = load_vec<V>(src(g * S::B_ + kk, 2, c * E));
   }
+  if (BWD) {
+    const T* dout = reinterpret_cast<const T*>(a.dout);
+    const T* out = reinterpret_cast<const T*>(a.out);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int e = lane + 64 * t, i = e / VPR, c = e % VPR;
+      const int row = min(g * S::B_ + i, a.n - 1);
+      const int64_t o = ((int64_t)bi * a.n + row) * dim + (int64_t)h * S::HD + c * E;
+      L.gv[t] = load_vec<V>(dout + o);
+      L.ov[t] = load_vec<V>(out + o);
+    }
+  }
+}
+
+// Store a unit's loads: the query block rotated (rows; transposed too for
+// the backward), the window keys rotated (rows; transposed for the
+// backward), the values (rows for the backward, transposed for the forward),
+// and for the backward dO (rows and transposed; zero beyond the n real rows)
+// and delta = rowsum(dO * O).
+template <typename T, bool BWD>
+__device__ __forceinline__ void store_unit(const HaloArgs& a, const HaloLoads<T>& L, int g, T* qs, T* qts, T* ks,
+                                           T* kts, T* vs, T* vts, T* dos, T* dots, float* delta) {
+  typedef HaloMfma S;
+  typedef typename Vec16<T>::type V;
+  constexpr int E = 8, VPR = S::HD / E, HV = VPR / 2;
+  const int lane = threadIdx.x;
   // rotate a (lo, hi) pair of 8-element chunks; store rows and, if asked, columns
   auto put = [&](const V& lo, const V& hi, const f32x4 (&cs)[2], const f32x4 (&sn)[2], int row, int c, T* rows,
                  T* cols, int ldc) {
@@ -689,62 +719,42 @@ __device__ __forceinline__ void stage_mfma(const HaloArgs& a, const T* qkv, int6
       }
     }
   };
-  put(ql, qh, qcs, qsn, qi, qc, qs, BWD ? qts : nullptr, S::LR);
+  put(L.ql, L.qh, L.qcs, L.qsn, lane / HV, lane % HV, qs, BWD ? qts : nullptr, S::LR);
 #pragma unroll
-  for (int t = 0; t < TK; ++t) {
+  for (int t = 0; t < 2; ++t) {
     const int e = lane + 64 * t;
-    put(kl[t], kh[t], kcs[t], ksn[t], e / HV, e % HV, ks, BWD ? kts : nullptr, S::LK);
+    put(L.kl[t], L.kh[t], L.kcs[t], L.ksn[t], e / HV, e % HV, ks, BWD ? kts : nullptr, S::LK);
   }
 #pragma unroll
-  for (int t = 0; t < TV; ++t) {
+  for (int t = 0; t < 4; ++t) {
     const int e = lane + 64 * t, kk = e / VPR, c = e % VPR;
     if (BWD) {
-      *reinterpret_cast<V*>(vs + kk * S::LD + c * E) = vv[t];
+      *reinterpret_cast<V*>(vs + kk * S::LD + c * E) = L.vv[t];
     } else {
 #pragma unroll
-      for (int u = 0; u < E; ++u) vts[(c * E + u) * S::LK + kk] = vv[t][u];
+      for (int u = 0; u < E; ++u) vts[(c * E + u) * S::LK + kk] = L.vv[t][u];
     }
   }
-}
-
-// dO rows of query block g (zero beyond the n real rows) as rows and
-// columns, and delta = rowsum(dO * O) from the same loads.
-template <typename T>
-__device__ __forceinline__ void stage_do_mfma(const HaloArgs& a, int bi, int h, int g, T* dos, T* dots,
-                                              float* delta) {
-  typedef HaloMfma S;
-  typedef typename Vec16<T>::type V;
-  constexpr int E = 8, VPR = S::HD / E, TT = S::B_ * VPR / 64;  // 2
-  const int lane = threadIdx.x;
-  const int64_t dim = (int64_t)a.H * S::HD;
-  const T* dout = reinterpret_cast<const T*>(a.dout);
-  const T* out = reinterpret_cast<const T*>(a.out);
-  V gv[TT], ov[TT];
+  if (BWD) {
 #pragma unroll
-  for (int t = 0; t < TT; ++t) {
-    const int e = lane + 64 * t, i = e / VPR, c = e % VPR;
-    const int row = min(g * S::B_ + i, a.n - 1);
-    const int64_t o = ((int64_t)bi * a.n + row) * dim + (int64_t)h * S::HD + c * E;
-    gv[t] = load_vec<V>(dout + o);
-    ov[t] = load_vec<V>(out + o);
-  }
+    for (int t = 0; t < 2; ++t) {
+      const int e = lane + 64 * t, i = e / VPR, c = e % VPR;
+      float sd = 0.f;
 #pragma unroll
-  for (int t = 0; t < TT; ++t) {
-    const int e = lane + 64 * t, i = e / VPR, c = e % VPR;
-    float sd = 0.f;
+      for (int u = 0; u < E; ++u) sd += to_float<T>(L.gv[t][u]) * to_float<T>(L.ov[t][u]);
 #pragma unroll
-    for (int u = 0; u < E; ++u) sd += to_float<T>(gv[t][u]) * to_float<T>(ov[t][u]);
+      for (int off = 1; off < VPR; off <<= 1) sd += __shfl_xor(sd, off, 64);
+      V gz = L.gv[t];
+      if (g * S::B_ + i >= a.n) {
+        sd = 0.f;
 #pragma unroll
-    for (int off = 1; off < VPR; off <<= 1) sd += __shfl_xor(sd, off, 64);
-    if (g * S::B_ + i >= a.n) {
-      sd = 0.f;
+        for (int u = 0; u < E; ++u) gz[u] = from_float<T>(0.f);
+      }
+      *reinterpret_cast<V*>(dos + i * S::LD + c * E) = gz;
 #pragma unroll
-      for (int u = 0; u < E; ++u) gv[t][u] = from_float<T>(0.f);
+      for (int u = 0; u < E; ++u) dots[(c * E + u) * S::LR + i] = gz[u];
+      if (c == 0) delta[i] = sd;
     }
-    *reinterpret_cast<V*>(dos + i * S::LD + c * E) = gv[t];
-#pragma unroll
-    for (int u = 0; u < E; ++u) dots[(c * E + u) * S::LR + i] = gv[t][u];
-    if (c == 0) delta[i] = sd;
   }
 }
 
@@ -840,7 +850,11 @@ __global__ __launch_bounds__(64) void halo_fwd_mfma_kernel(HaloArgs a) {
   const int g = (int)((blockIdx.x / (unsigned)a.H) % (unsigned)a.G);
   const int bi = (int)(blockIdx.x / ((unsigned)a.H * (unsigned)a.G));
   const int64_t row0 = (int64_t)bi * (a.G + 1) * S::B_;
-  stage_mfma<T, false>(a, reinterpret_cast<const T*>(a.qkv), row0, h, g, qs, nullptr, ks, nullptr, nullptr, vts);
+  {
+    HaloLoads<T> L;
+    load_unit<T, false>(a, row0, bi, h, g, L);
+    store_unit<T, false>(a, L, g, qs, nullptr, ks, nullptr, nullptr, vts, nullptr, nullptr, nullptr);
+  }
   __syncthreads();
   f32x4 p[2];
   window_tiles<T>(ks, qs, p);
@@ -875,7 +889,6 @@ __global__ __launch_bounds__(64) void halo_bwd_mfma_kernel(HaloArgs a) {
   const int bi = (int)(blockIdx.x / ((unsigned)a.H * (unsigned)(a.G + 1)));
   const int64_t row0 = (int64_t)bi * (a.G + 1) * S::B_;
   const int64_t dim = (int64_t)a.H * S::HD;
-  const T* qkv = reinterpret_cast<const T*>(a.qkv);
   T* dqkv = reinterpret_cast<T*>(a.dqkv);
   auto at = [&](int row, int slot, int d) { return ((row0 + row) * 3 + slot) * dim + (int64_t)h * S::HD + d; };
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
@@ -889,13 +902,17 @@ __global__ __launch_bounds__(64) void halo_bwd_mfma_kernel(HaloArgs a) {
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) dk[dt] = dv[dt] = zero;
 
+  // role 0: own block of query block r-1; role 1: previous block of query
+  // block r. (Loading the second role's tiles during the first role's
+  // products measured slower: the registers held across them.)
+  const int role0 = r == 0 ? 1 : 0, role1 = r == a.G ? 0 : 1;  // a.G >= 1: at least one role
 #pragma unroll 1
-  for (int role = 0; role < 2; ++role) {
-    const int g = role == 0 ? r - 1 : r;  // role 0: own block of query block r-1; role 1: previous of query block r
-    if (g < 0 || g >= a.G) continue;      // uniform over the wave
+  for (int role = role0; role <= role1; ++role) {
+    const int g = role == 0 ? r - 1 : r;
+    HaloLoads<T> L;
+    load_unit<T, true>(a, row0, bi, h, g, L);  // registers only: before the barrier
     __syncthreads();
-    stage_mfma<T, true>(a, qkv, row0, h, g, qs, qts, ks, kts, vs, nullptr);
-    stage_do_mfma<T>(a, bi, h, g, dos, dots, delta);
+    store_unit<T, true>(a, L, g, qs, qts, ks, kts, vs, nullptr, dos, dots, delta);
     __syncthreads();
     f32x4 p[2], ds[2];
     window_tiles<T>(ks, qs, p);
