@@ -62,6 +62,14 @@ def test_fused_window_attention(device, b, hd, heads, n, start, halo, dtype):
         assert_close(ggot[name], gwant[name], dtype, name)
 
 
+@pytest.mark.parametrize("b,hd,heads", [(16, 64, 4), (8, 64, 2), (16, 128, 2)])
+@pytest.mark.parametrize("n,start,halo", [(96, 0, False), (83, 48, True)])
+def test_fused_window_attention_fp16(device, b, hd, heads, n, start, halo):
+    """fp16 through the same kernels (MFMA at b 16, head_dim 64; VALU
+    otherwise), against the PyTorch path in fp32."""
+    test_fused_window_attention(device, b, hd, heads, n, start, halo, torch.float16)
+
+
 def test_unsupported_shape_keeps_pytorch_path(device):
     """A head_dim without a kernel runs the PyTorch attention."""
     layer = _block(48, 2, 16, device, torch.float32)  # head_dim 24
