@@ -621,8 +621,7 @@ __global__ __launch_bounds__(64) void halo_bwd64_kernel(HaloArgs a) {
 struct HaloMfma {
   static constexpr int B_ = 16, W = 32, HD = 64, HALF = 32;
   static constexpr int LD = HD + 8;  // row-major 16-bit tiles (144-byte rows)
-  static constexpr int LK = W + 8;   // transposed K / V: [d][key]
-  static constexpr int LR = B_ + 8;  // transposed Q / dO: [d][row]; P^T, dS^T: [key][row]
+  static constexpr int LR = B_ + 8;  // P^T, dS^T: [key][row]
 };
 
 template <typename T>
@@ -686,21 +685,19 @@ __device__ __forceinline__ void load_unit(const HaloArgs& a, int64_t row0, int b
   }
 }
 
-// Store a unit's loads: the query block rotated (rows; transposed too for
-// the backward), the window keys rotated (rows; transposed for the
-// backward), the values (rows for the backward, transposed for the forward),
-// and for the backward dO (rows and transposed; zero beyond the n real rows)
-// and delta = rowsum(dO * O).
+// Store a unit's loads as row-major tiles: the query block and its window
+// keys rotated, the values, and for the backward dO (zero beyond the n real
+// rows) and delta = rowsum(dO * O). Operands that need the transpose read
+// these tiles with ds_read_tr16_b64 (frag_tr_rows).
 template <typename T, bool BWD>
-__device__ __forceinline__ void store_unit(const HaloArgs& a, const HaloLoads<T>& L, int g, T* qs, T* qts, T* ks,
-                                           T* kts, T* vs, T* vts, T* dos, T* dots, float* delta) {
+__device__ __forceinline__ void store_unit(const HaloArgs& a, const HaloLoads<T>& L, int g, T* qs, T* ks, T* vs,
+                                           T* dos, float* delta) {
   typedef HaloMfma S;
   typedef typename Vec16<T>::type V;
   constexpr int E = 8, VPR = S::HD / E, HV = VPR / 2;
   const int lane = threadIdx.x;
-  // rotate a (lo, hi) pair of 8-element chunks; store rows and, if asked, columns
-  auto put = [&](const V& lo, const V& hi, const f32x4 (&cs)[2], const f32x4 (&sn)[2], int row, int c, T* rows,
-                 T* cols, int ldc) {
+  // rotate a (lo, hi) pair of 8-element chunks of one row
+  auto put = [&](const V& lo, const V& hi, const f32x4 (&cs)[2], const f32x4 (&sn)[2], int row, int c, T* rows) {
     V lo_out, hi_out;
 #pragma unroll
     for (int u = 0; u < E; ++u) {
@@ -711,29 +708,17 @@ __device__ __forceinline__ void store_unit(const HaloArgs& a, const HaloLoads<T>
     }
     *reinterpret_cast<V*>(rows + row * S::LD + c * E) = lo_out;
     *reinterpret_cast<V*>(rows + row * S::LD + c * E + S::HALF) = hi_out;
-    if (cols) {
-#pragma unroll
-      for (int u = 0; u < E; ++u) {
-        cols[(c * E + u) * ldc + row] = lo_out[u];
-        cols[(c * E + u + S::HALF) * ldc + row] = hi_out[u];
-      }
-    }
   };
-  put(L.ql, L.qh, L.qcs, L.qsn, lane / HV, lane % HV, qs, BWD ? qts : nullptr, S::LR);
+  put(L.ql, L.qh, L.qcs, L.qsn, lane / HV, lane % HV, qs);
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int e = lane + 64 * t;
-    put(L.kl[t], L.kh[t], L.kcs[t], L.ksn[t], e / HV, e % HV, ks, BWD ? kts : nullptr, S::LK);
+    put(L.kl[t], L.kh[t], L.kcs[t], L.ksn[t], e / HV, e % HV, ks);
   }
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const int e = lane + 64 * t, kk = e / VPR, c = e % VPR;
-    if (BWD) {
-      *reinterpret_cast<V*>(vs + kk * S::LD + c * E) = L.vv[t];
-    } else {
-#pragma unroll
-      for (int u = 0; u < E; ++u) vts[(c * E + u) * S::LK + kk] = L.vv[t][u];
-    }
+    *reinterpret_cast<V*>(vs + kk * S::LD + c * E) = L.vv[t];
   }
   if (BWD) {
 #pragma unroll
@@ -751,8 +736,6 @@ __device__ __forceinline__ void store_unit(const HaloArgs& a, const HaloLoads<T>
         for (int u = 0; u < E; ++u) gz[u] = from_float<T>(0.f);
       }
       *reinterpret_cast<V*>(dos + i * S::LD + c * E) = gz;
-#pragma unroll
-      for (int u = 0; u < E; ++u) dots[(c * E + u) * S::LR + i] = gz[u];
       if (c == 0) delta[i] = sd;
     }
   }
@@ -825,26 +808,30 @@ __device__ __forceinline__ typename Mma16<T>::Frag pack_rows(const f32x4 (&x)[2]
   return f;
 }
 
-// B operand (key slots in the permuted order, column d) from a transposed
-// [d][key] tile.
+// B operand of a 16x16x32 product for columns [d0, d0 + 16), read from a
+// row-major tile X (stride LD) with two ds_read_tr16_b64: k slots 8(l/16) +
+// {0..3} take rows r_lo + {0..3} and slots 8(l/16) + {4..7} rows r_hi +
+// {0..3}, column d0 + l%16. Within a 16-lane group the instruction returns to
+// lane i element i%4 of the 8 bytes that lanes 4j + i/4 (j = 0..3) address,
+// so lane s addresses row r + s/4, columns d0 + 4(s%4)..+3.
 template <typename T>
-__device__ __forceinline__ typename Mma16<T>::Frag frag_keys(const T* ts, int d, int grp) {
-  const Vec4<T> lo = *reinterpret_cast<const Vec4<T>*>(ts + d * HaloMfma::LK + 4 * grp);
-  const Vec4<T> hi = *reinterpret_cast<const Vec4<T>*>(ts + d * HaloMfma::LK + 16 + 4 * grp);
-  typename Mma16<T>::Frag f;
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    f[u] = lo[u];
-    f[u + 4] = hi[u];
-  }
-  return f;
+__device__ __forceinline__ typename Mma16<T>::Frag frag_tr_rows(const T* x, int r_lo, int r_hi, int d0) {
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  typedef short s8 __attribute__((ext_vector_type(8)));
+  const int s = threadIdx.x & 15;
+  const T* p0 = x + (r_lo + (s >> 2)) * HaloMfma::LD + d0 + 4 * (s & 3);
+  const T* p1 = x + (r_hi + (s >> 2)) * HaloMfma::LD + d0 + 4 * (s & 3);
+  const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)p0);
+  const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)p1);
+  const s8 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(typename Mma16<T>::Frag, v);
 }
 
 template <typename T>
 __global__ __launch_bounds__(64) void halo_fwd_mfma_kernel(HaloArgs a) {
   typedef HaloMfma S;
   typedef Mma16<T> M;
-  __shared__ __attribute__((aligned(16))) T qs[S::B_ * S::LD], ks[S::W * S::LD], vts[S::HD * S::LK];
+  __shared__ __attribute__((aligned(16))) T qs[S::B_ * S::LD], ks[S::W * S::LD], vs[S::W * S::LD];
   const int lane = threadIdx.x, col = lane & 15, grp = lane >> 4;
   const int h = (int)(blockIdx.x % (unsigned)a.H);
   const int g = (int)((blockIdx.x / (unsigned)a.H) % (unsigned)a.G);
@@ -853,7 +840,7 @@ __global__ __launch_bounds__(64) void halo_fwd_mfma_kernel(HaloArgs a) {
   {
     HaloLoads<T> L;
     load_unit<T, false>(a, row0, bi, h, g, L);
-    store_unit<T, false>(a, L, g, qs, nullptr, ks, nullptr, nullptr, vts, nullptr, nullptr, nullptr);
+    store_unit<T, false>(a, L, g, qs, ks, vs, nullptr, nullptr);
   }
   __syncthreads();
   f32x4 p[2];
@@ -864,7 +851,7 @@ __global__ __launch_bounds__(64) void halo_fwd_mfma_kernel(HaloArgs a) {
   const int64_t dim = (int64_t)a.H * S::HD;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
-    const f32x4 o = M::mma(pa, frag_keys<T>(vts, 16 * dt + col, grp), f32x4{0.f, 0.f, 0.f, 0.f});
+    const f32x4 o = M::mma(pa, frag_tr_rows<T>(vs, 4 * grp, 16 + 4 * grp, 16 * dt), f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = g * S::B_ + 4 * grp + r;
@@ -880,7 +867,6 @@ __global__ __launch_bounds__(64) void halo_bwd_mfma_kernel(HaloArgs a) {
   typedef typename M::Frag F;
   __shared__ __attribute__((aligned(16))) T qs[S::B_ * S::LD], ks[S::W * S::LD], vs[S::W * S::LD];
   __shared__ __attribute__((aligned(16))) T dos[S::B_ * S::LD];
-  __shared__ __attribute__((aligned(16))) T qts[S::HD * S::LR], kts[S::HD * S::LK], dots[S::HD * S::LR];
   __shared__ __attribute__((aligned(16))) T pts[S::B_ * S::LR], dsts[S::B_ * S::LR];
   __shared__ float delta[S::B_];
   const int lane = threadIdx.x, col = lane & 15, grp = lane >> 4;
@@ -912,7 +898,7 @@ __global__ __launch_bounds__(64) void halo_bwd_mfma_kernel(HaloArgs a) {
     HaloLoads<T> L;
     load_unit<T, true>(a, row0, bi, h, g, L);  // registers only: before the barrier
     __syncthreads();
-    store_unit<T, true>(a, L, g, qs, qts, ks, kts, vs, nullptr, dos, dots, delta);
+    store_unit<T, true>(a, L, g, qs, ks, vs, dos, delta);
     __syncthreads();
     f32x4 p[2], ds[2];
     window_tiles<T>(ks, qs, p);
@@ -926,7 +912,7 @@ __global__ __launch_bounds__(64) void halo_bwd_mfma_kernel(HaloArgs a) {
       const F da = pack_rows<T>(ds);
       f32x4 y[4];
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) y[dt] = M::mma(da, frag_keys<T>(kts, 16 * dt + col, grp), zero);
+      for (int dt = 0; dt < 4; ++dt) y[dt] = M::mma(da, frag_tr_rows<T>(ks, 4 * grp, 16 + 4 * grp, 16 * dt), zero);
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt) {
 #pragma unroll
@@ -950,12 +936,12 @@ __global__ __launch_bounds__(64) void halo_bwd_mfma_kernel(HaloArgs a) {
     const bool kin = grp < 2;  // k slots 0..15: the 16 query rows
     const F pa = kin ? *reinterpret_cast<const F*>(pts + col * S::LR + 8 * grp) : fzero;
     const F sa = kin ? *reinterpret_cast<const F*>(dsts + col * S::LR + 8 * grp) : fzero;
+    const int rb = 8 * (grp & 1);  // lanes 32..63 read rows 0..15 too, then use zeros
     f32x4 kt[4];
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
-      const int d = 16 * dt + col;
-      const F ob = kin ? *reinterpret_cast<const F*>(dots + d * S::LR + 8 * grp) : fzero;
-      const F qb = kin ? *reinterpret_cast<const F*>(qts + d * S::LR + 8 * grp) : fzero;
+      const F ob_r = frag_tr_rows<T>(dos, rb, rb + 4, 16 * dt), qb_r = frag_tr_rows<T>(qs, rb, rb + 4, 16 * dt);
+      const F ob = kin ? ob_r : fzero, qb = kin ? qb_r : fzero;
       dv[dt] = M::mma(pa, ob, dv[dt]);
       kt[dt] = M::mma(sa, qb, zero);
     }
