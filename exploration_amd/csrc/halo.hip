@@ -860,8 +860,12 @@ __global__ __launch_bounds__(64) void halo_fwd_mfma_kernel(HaloArgs a) {
   }
 }
 
+// Two waves per SIMD (at most 256 registers): each wave's staging loads wait
+// while the other computes. The compiler then spills a few registers (16-32
+// bytes of scratch per lane); measured at stack_100m's shape that is still
+// far faster than one wave per SIMD without spills (50 against 68 us).
 template <typename T>
-__global__ __launch_bounds__(64) void halo_bwd_mfma_kernel(HaloArgs a) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void halo_bwd_mfma_kernel(HaloArgs a) {
   typedef HaloMfma S;
   typedef Mma16<T> M;
   typedef typename M::Frag F;
@@ -877,6 +881,17 @@ __global__ __launch_bounds__(64) void halo_bwd_mfma_kernel(HaloArgs a) {
   const int64_t dim = (int64_t)a.H * S::HD;
   T* dqkv = reinterpret_cast<T*>(a.dqkv);
   auto at = [&](int row, int slot, int d) { return ((row0 + row) * 3 + slot) * dim + (int64_t)h * S::HD + d; };
+  // the 16 x 64 row tile x (stride LD, written by this wave) to block r's
+  // rows of slot: 128 16-byte chunks, two per lane
+  auto store_rows = [&](const T* x, int slot) {
+    typedef typename Vec16<T>::type V;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int e = lane + 64 * t, row = e / 8, c = e % 8;
+      *reinterpret_cast<V*>(dqkv + at(r * S::B_ + row, slot, c * 8)) =
+          *reinterpret_cast<const V*>(x + row * S::LD + c * 8);
+    }
+  };
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   F fzero;
 #pragma unroll
@@ -908,7 +923,9 @@ __global__ __launch_bounds__(64) void halo_bwd_mfma_kernel(HaloArgs a) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) ds[t] = p[t] * (ds[t] - dl);
     if (role == 0) {
-      // dq of block r = scale dS K, through the query rotary transpose
+      // dq of block r = scale dS K, through the query rotary transpose; the
+      // rows go through LDS (the V rows are dead once dP^T is formed) and
+      // leave as 16-byte stores
       const F da = pack_rows<T>(ds);
       f32x4 y[4];
 #pragma unroll
@@ -920,10 +937,11 @@ __global__ __launch_bounds__(64) void halo_bwd_mfma_kernel(HaloArgs a) {
           const int row = 4 * grp + i, d = 16 * dt + col;
           const float cs = a.cos_t[(S::B_ + row) * S::HALF + d], sn = a.sin_t[(S::B_ + row) * S::HALF + d];
           const float lo = a.scale * y[dt][i], hi = a.scale * y[dt + 2][i];
-          dqkv[at(r * S::B_ + row, 0, d)] = from_float<T>(lo * cs + hi * sn);
-          dqkv[at(r * S::B_ + row, 0, d + S::HALF)] = from_float<T>(hi * cs - lo * sn);
+          vs[row * S::LD + d] = from_float<T>(lo * cs + hi * sn);
+          vs[row * S::LD + d + S::HALF] = from_float<T>(hi * cs - lo * sn);
         }
       }
+      store_rows(vs, 0);
     }
     // this role's window keys kk0 + j are block r's rows j
     const int th = role == 0 ? 1 : 0, kk0 = 16 * th;
@@ -957,14 +975,28 @@ __global__ __launch_bounds__(64) void halo_bwd_mfma_kernel(HaloArgs a) {
       }
     }
   }
+  // dk, dv (and the zero dq of block 0) through the Q and dO row tiles,
+  // free after the last role's products
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int row = r * S::B_ + 4 * grp + i, d = 16 * dt + col;
-      if (r == 0) dqkv[at(row, 0, d)] = from_float<T>(0.f);
-      dqkv[at(row, 1, d)] = from_float<T>(dk[dt][i]);
-      dqkv[at(row, 2, d)] = from_float<T>(dv[dt][i]);
+      const int row = 4 * grp + i, d = 16 * dt + col;
+      qs[row * S::LD + d] = from_float<T>(dk[dt][i]);
+      dos[row * S::LD + d] = from_float<T>(dv[dt][i]);
+    }
+  }
+  store_rows(qs, 1);
+  store_rows(dos, 2);
+  if (r == 0) {
+    typedef typename Vec16<T>::type V;
+    V z;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) z[u] = from_float<T>(0.f);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int e = lane + 64 * t;
+      *reinterpret_cast<V*>(dqkv + at(e / 8, 0, (e % 8) * 8)) = z;
     }
   }
 }
