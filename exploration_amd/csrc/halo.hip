@@ -847,16 +847,23 @@ __global__ __launch_bounds__(64) void halo_fwd_mfma_kernel(HaloArgs a) {
   window_tiles<T>(ks, qs, p);
   window_softmax(a, g, p);
   const typename M::Frag pa = pack_rows<T>(p);
-  T* out = reinterpret_cast<T*>(a.out);
-  const int64_t dim = (int64_t)a.H * S::HD;
+  // the context rows go through the query tile (dead after the scores) and
+  // leave as 16-byte stores
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
     const f32x4 o = M::mma(pa, frag_tr_rows<T>(vs, 4 * grp, 16 + 4 * grp, 16 * dt), f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = g * S::B_ + 4 * grp + r;
-      if (t < a.n) out[((int64_t)bi * a.n + t) * dim + (int64_t)h * S::HD + 16 * dt + col] = from_float<T>(o[r]);
-    }
+    for (int r = 0; r < 4; ++r) qs[(4 * grp + r) * S::LD + 16 * dt + col] = from_float<T>(o[r]);
+  }
+  typedef typename Vec16<T>::type V;
+  T* out = reinterpret_cast<T*>(a.out);
+  const int64_t dim = (int64_t)a.H * S::HD;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int e = lane + 64 * t, row = e / 8, c = e % 8, tok = g * S::B_ + row;
+    if (tok < a.n)
+      *reinterpret_cast<V*>(out + ((int64_t)bi * a.n + tok) * dim + (int64_t)h * S::HD + c * 8) =
+          *reinterpret_cast<const V*>(qs + row * S::LD + c * 8);
   }
 }
 
