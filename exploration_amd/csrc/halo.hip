@@ -638,7 +638,9 @@ struct HaloLoads {
   f32x4 qcs[2], qsn[2], kcs[2][2], ksn[2][2];
 };
 
-template <typename T, bool BWD>
+// PARTS selects what to load / store: bit 0 the query block and window keys
+// (with their cos/sin), bit 1 the values and, for the backward, dO and O.
+template <typename T, bool BWD, int PARTS = 3>
 __device__ __forceinline__ void load_unit(const HaloArgs& a, int64_t row0, int bi, int h, int g, HaloLoads<T>& L) {
   typedef HaloMfma S;
   typedef typename Vec16<T>::type V;
@@ -648,6 +650,7 @@ __device__ __forceinline__ void load_unit(const HaloArgs& a, int64_t row0, int b
   const T* qkv = reinterpret_cast<const T*>(a.qkv);
   auto src = [&](int r, int slot, int d) { return qkv + ((row0 + r) * 3 + slot) * dim + (int64_t)h * S::HD + d; };
   const int qi = lane / HV, qc = lane % HV;
+  if constexpr (PARTS & 1) {
   L.ql = load_vec<V>(src((g + 1) * S::B_ + qi, 0, qc * E));
   L.qh = load_vec<V>(src((g + 1) * S::B_ + qi, 0, qc * E + S::HALF));
 #pragma unroll
@@ -666,12 +669,15 @@ __device__ __forceinline__ void load_unit(const HaloArgs& a, int64_t row0, int b
       L.ksn[t][u] = load_vec<f32x4>(a.sin_t + kk * S::HALF + c * E + 4 * u);
     }
   }
+  }
+  if constexpr ((PARTS & 2) != 0) {
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const int e = lane + 64 * t, kk = e / VPR, c = e % VPR;
     L.vv[t] = load_vec<V>(src(g * S::B_ + kk, 2, c * E));
   }
-  if (BWD) {
+  }
+  if (BWD && (PARTS & 2)) {
     const T* dout = reinterpret_cast<const T*>(a.dout);
     const T* out = reinterpret_cast<const T*>(a.out);
 #pragma unroll
@@ -689,7 +695,7 @@ __device__ __forceinline__ void load_unit(const HaloArgs& a, int64_t row0, int b
 // keys rotated, the values, and for the backward dO (zero beyond the n real
 // rows) and delta = rowsum(dO * O). Operands that need the transpose read
 // these tiles with ds_read_tr16_b64 (frag_tr_rows).
-template <typename T, bool BWD>
+template <typename T, bool BWD, int PARTS = 3>
 __device__ __forceinline__ void store_unit(const HaloArgs& a, const HaloLoads<T>& L, int g, T* qs, T* ks, T* vs,
                                            T* dos, float* delta) {
   typedef HaloMfma S;
@@ -709,18 +715,22 @@ __device__ __forceinline__ void store_unit(const HaloArgs& a, const HaloLoads<T>
     *reinterpret_cast<V*>(rows + row * S::LD + c * E) = lo_out;
     *reinterpret_cast<V*>(rows + row * S::LD + c * E + S::HALF) = hi_out;
   };
-  put(L.ql, L.qh, L.qcs, L.qsn, lane / HV, lane % HV, qs);
+  if constexpr (PARTS & 1) {
+    put(L.ql, L.qh, L.qcs, L.qsn, lane / HV, lane % HV, qs);
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int e = lane + 64 * t;
-    put(L.kl[t], L.kh[t], L.kcs[t], L.ksn[t], e / HV, e % HV, ks);
+    for (int t = 0; t < 2; ++t) {
+      const int e = lane + 64 * t;
+      put(L.kl[t], L.kh[t], L.kcs[t], L.ksn[t], e / HV, e % HV, ks);
+    }
   }
+  if constexpr ((PARTS & 2) != 0) {
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int e = lane + 64 * t, kk = e / VPR, c = e % VPR;
-    *reinterpret_cast<V*>(vs + kk * S::LD + c * E) = L.vv[t];
+    for (int t = 0; t < 4; ++t) {
+      const int e = lane + 64 * t, kk = e / VPR, c = e % VPR;
+      *reinterpret_cast<V*>(vs + kk * S::LD + c * E) = L.vv[t];
+    }
   }
-  if (BWD) {
+  if (BWD && (PARTS & 2)) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int e = lane + 64 * t, i = e / VPR, c = e % VPR;
@@ -868,9 +878,9 @@ __global__ __launch_bounds__(64) void halo_fwd_mfma_kernel(HaloArgs a) {
 }
 
 // Two waves per SIMD (at most 256 registers): each wave's staging loads wait
-// while the other computes. The compiler then spills a few registers (16-32
-// bytes of scratch per lane); measured at stack_100m's shape that is still
-// far faster than one wave per SIMD without spills (50 against 68 us).
+// while the other computes (at stack_100m's shape 50 us, against 68 us at
+// one wave per SIMD). Staging in two load phases keeps it within the limit
+// without spills.
 template <typename T>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void halo_bwd_mfma_kernel(HaloArgs a) {
   typedef HaloMfma S;
@@ -918,9 +928,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void ha
   for (int role = role0; role <= role1; ++role) {
     const int g = role == 0 ? r - 1 : r;
     HaloLoads<T> L;
-    load_unit<T, true>(a, row0, bi, h, g, L);  // registers only: before the barrier
+    // two load phases (queries and keys, then values, dO and O) keep fewer
+    // registers in flight; the other wave on the SIMD covers the latency
+    load_unit<T, true, 1>(a, row0, bi, h, g, L);  // registers only: before the barrier
     __syncthreads();
-    store_unit<T, true>(a, L, g, qs, ks, vs, dos, delta);
+    store_unit<T, true, 1>(a, L, g, qs, ks, vs, dos, delta);
+    load_unit<T, true, 2>(a, row0, bi, h, g, L);
+    store_unit<T, true, 2>(a, L, g, qs, ks, vs, dos, delta);
     __syncthreads();
     f32x4 p[2], ds[2];
     window_tiles<T>(ks, qs, p);
