@@ -137,6 +137,16 @@ def test_cfg2_full_size(device):
     _check_dense(q, k, v, pos, do, b, device, torch.bfloat16, oracle_device=device, label="cfg2")
 
 
+def test_cfg2_every_row_at_the_last_position(device):
+    """cfg2's tensors with every query at position 4095 (all keys visible, no
+    causal structure: the `bench.py --dense-rows last` workload), in pair
+    mode with equal-length row tiles (oracle in float32 on the GPU)."""
+    print("dense cfg2 rows at the last position", flush=True)
+    q, k, v, pos, do, b = dense_config(CFG2, device=device)
+    pos = torch.full_like(pos, k.shape[1] - 1)
+    _check_dense(q, k, v, pos, do, b, device, torch.bfloat16, oracle_device=device, label="cfg2-last")
+
+
 @pytest.mark.parametrize("d,b,tiles", [(64, 64, 33), (128, 128, 32), (128, 16, 34)])
 def test_causal_pair_mode(device, d, b, tiles):
     """Causal rows over enough 128-row tiles (B1 H8) that the forward pairs
