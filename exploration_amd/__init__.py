@@ -15,8 +15,13 @@ from .sparse import PagedKV, TensorPages, block_scores, select_blocks, sparse_at
 
 
 def launch_report():
-    from . import attention, sparse
-    return attention.launch_report() + sparse.launch_report()
+    """Operator-level records (kernel = operator, with dtype, head_dim and
+    block size) followed by the library's per-kernel launch records (tiles,
+    waves, LDS buffers, registers, LDS bytes, workgroups; the reference's
+    ``st/ops/kernels/launch.py:52-56`` fields)."""
+    from . import _lib, attention, sparse
+    native = _lib.native_launch_report() if _lib._lib is not None else []
+    return attention.launch_report() + sparse.launch_report() + native
 
 
 __all__ = ["dense_attention", "dense_hip", "hip_supported", "triton_supported", "sparse_attention",

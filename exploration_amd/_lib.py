@@ -22,6 +22,7 @@ _i64, _p, _f32p, _i64p, _i32p, _sz = (ctypes.c_int64, ctypes.c_void_p, ctypes.c_
 SIGNATURES = {
     "st_abi_version": (ctypes.c_int, []),
     "st_last_error": (ctypes.c_char_p, []),
+    "st_launch_report": (_sz, [ctypes.c_char_p, _sz]),
     "st_dense_supported": (ctypes.c_int, [ctypes.c_int, _i64, _i64]),
     "st_dense_fwd_workspace_bytes": (_sz, [ctypes.c_int] + [_i64] * 6),
     "st_dense_fwd": (ctypes.c_int, [ctypes.c_int] + [_i64] * 6 + [_p] * 3 + [_i64p, _p] + [_f32p] * 4
@@ -34,7 +35,7 @@ SIGNATURES = {
     "st_sparse_select": (ctypes.c_int, [_i64] * 4 + [_f32p, _i64p, _f32p, _f32p, _p]),
     "st_sparse_workspace_bytes": (_sz, [_i64] * 6),
     "st_sparse_pop": (ctypes.c_int, [ctypes.c_int] + [_i64] * 5 + [_p, _i64p, _p, _p, _i32p] + [_i64] * 4
-                      + [_i64p, _f32p, _f32p, _i64, _p, _f32p, _p, _sz, _p]),
+                      + [_i64p, _f32p, _f32p, _i64, ctypes.c_int, _p, _f32p, _p, _sz, _p]),
     "st_sparse_fwd": (ctypes.c_int, [ctypes.c_int] + [_i64] * 6 + [_p, _i64p, _p, _p, _i32p] + [_i64] * 4
                       + [_p, _i64p, _f32p, _f32p, _f32p, _p, _sz, _p]),
     "st_halo_supported": (ctypes.c_int, [ctypes.c_int, _i64, _i64]),
@@ -42,7 +43,7 @@ SIGNATURES = {
     "st_halo_attn_bwd": (ctypes.c_int, [ctypes.c_int] + [_i64] * 8 + [_p, _f32p, _f32p, _p, _p, _p, _p]),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 _lib = None
 
 
@@ -82,6 +83,21 @@ def check(status, lib=None):
     if status in (ST_EINVAL, ST_EUNSUPPORTED):
         raise ValueError(msg)
     raise RuntimeError(msg)
+
+
+def native_launch_report():
+    """The library's launch records (``st_launch_report``) as a list of dicts."""
+    import json
+
+    lib = load()
+    need = lib.st_launch_report(None, 0)
+    buf = ctypes.create_string_buffer(need)
+    lib.st_launch_report(buf, need)
+    codes = {v: str(k) for k, v in DTYPE_CODES.items()}
+    records = json.loads(buf.value.decode())
+    for r in records:
+        r["dtype"] = codes.get(r["dtype"], r["dtype"])
+    return records
 
 
 def ptr(t):

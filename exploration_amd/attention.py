@@ -40,11 +40,13 @@ def hip_supported(q, block_size):
     """Whether the fused HIP kernels handle this query tensor and block size
     (the reference's ``triton_supported``, ``st/ops/attention.py:142-145``):
     a ROCm device tensor in fp32/fp16/bf16, ``block_size`` a power of two in
-    [2, 128], ``head_dim <= 256`` and a multiple of 8."""
+    [2, 128] and ``head_dim <= 256`` (head dimensions that are not a
+    multiple of 8 run on zero-padded rows, as the reference pads D to a power
+    of two inside its kernel, ``st/ops/kernels/dense.py:210``)."""
     if not (isinstance(q, torch.Tensor) and q.is_cuda and q.dtype in _lib.DTYPE_CODES):
         return False
     b = int(block_size)
-    return 2 <= b <= 128 and b & (b - 1) == 0 and q.shape[-1] <= 256 and q.shape[-1] % 8 == 0
+    return 2 <= b <= 128 and b & (b - 1) == 0 and 1 <= q.shape[-1] <= 256
 
 
 # The reference's name for the capability predicate.
@@ -116,10 +118,13 @@ def dense_forward_stats(q, k, v, positions, block_size):
         return ctx.saved[4:]
 
 
-def dense_hip(q, k, v, positions, block_size):
+def dense_hip(q, k, v, positions, block_size, *, force_streamed=False):
     """Fused forward (autograd-aware) with the reference's internal signature
-    ``dense_triton(q, k, v, positions, block_size)``
-    (``st/ops/kernels/dense.py:236-239``)."""
+    ``dense_triton(q, k, v, positions, block_size, *, force_streamed=False)``
+    (``st/ops/kernels/dense.py:236-239``). ``force_streamed`` selects the
+    reference's small-tile fallback for NVIDIA shared-memory limits
+    (``st/ops/kernels/streamed.py``); every supported configuration fits the
+    LDS of one compute unit here, so both settings run the same kernels."""
     if q.dtype != k.dtype or q.dtype != v.dtype:
         raise ValueError("q/k/v must use the same dtype")
     if not (k.device == q.device and v.device == q.device and positions.device == q.device):
@@ -142,7 +147,7 @@ def dense_attention(q, k, v, positions, block_size, backend="auto", q_chunk=32, 
                          "this package only provides the fused HIP kernels")
     if not hip_supported(q, block_size):
         raise ValueError("the HIP kernels require ROCm fp16/bf16/fp32 tensors, head_dim <= 256 "
-                         "and a multiple of 8, and a power-of-two block_size in 2..128")
+                         "and a power-of-two block_size in 2..128")
     # Kernel arithmetic is fp32-accumulated regardless of autocast.
     with torch.autocast(q.device.type, enabled=False):
         return dense_hip(q, k, v, positions, block_size)

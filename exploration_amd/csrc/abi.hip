@@ -12,6 +12,8 @@
 #include "dense.h"
 #include "sparse.h"
 #include "halo.h"
+#include "pad.h"
+#include "report.h"
 
 namespace {
 
@@ -56,9 +58,8 @@ int check_envelope(int64_t head_dim, int64_t block_size) {
   if (!pow2(block_size) || block_size < 2 || block_size > 128)
     return fail(ST_EUNSUPPORTED, "block_size %lld: the fused kernels need a power of two in [2, 128]",
                 (long long)block_size);
-  if (head_dim > 256 || head_dim % 8 != 0)
-    return fail(ST_EUNSUPPORTED, "head_dim %lld: the fused kernels need head_dim <= 256 and a multiple of 8",
-                (long long)head_dim);
+  if (head_dim < 1 || head_dim > 256)
+    return fail(ST_EUNSUPPORTED, "head_dim %lld: the fused kernels need 1 <= head_dim <= 256", (long long)head_dim);
   return ST_OK;
 }
 
@@ -76,11 +77,70 @@ hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+size_t elem_bytes(int dtype) { return dtype == ST_DTYPE_F32 ? 4 : 2; }
+
+// Workspace of st_dense_fwd: the kernels' own (plan, at the padded head
+// dimension Dp) and, when Dp != D, zero-padded copies of q, k, v and of the
+// outputs out and rc.
+struct FwdLayout {
+  st::DenseFwdPlan plan;
+  int64_t Dp;
+  size_t off_q, off_k, off_v, off_out, off_rc, total;
+};
+
+FwdLayout dense_fwd_layout(int dtype, int64_t B, int64_t Q, int64_t N, int64_t H, int64_t D) {
+  FwdLayout l = {};
+  l.Dp = st::padded_head_dim(D);
+  l.plan = st::dense_fwd_plan(dtype, B, Q, N, H, l.Dp);
+  l.total = l.plan.total;
+  if (l.Dp == D) return l;
+  const size_t e = elem_bytes(dtype), rq = (size_t)(B * Q * H) * l.Dp, rk = (size_t)(B * N * H) * l.Dp;
+  size_t o = align256(l.total);
+  l.off_q = o; o += align256(rq * e);
+  l.off_k = o; o += align256(rk * e);
+  l.off_v = o; o += align256(rk * e);
+  l.off_out = o; o += align256(rq * e);
+  l.off_rc = o; o += align256(rq * 4);
+  l.total = o;
+  return l;
+}
+
+// Workspace of st_dense_bwd: the kernels' own and, when Dp != D, padded
+// copies of q, k, v, out, dout, rc and of the gradients.
+struct BwdLayout {
+  st::DenseBwdPlan plan;
+  int64_t Dp;
+  size_t off_q, off_k, off_v, off_out, off_dout, off_rc, off_dq, off_dk, off_dv, total;
+};
+
+BwdLayout dense_bwd_layout(int dtype, int64_t B, int64_t Q, int64_t N, int64_t H, int64_t D, int64_t b) {
+  BwdLayout l = {};
+  l.Dp = st::padded_head_dim(D);
+  l.plan = st::dense_bwd_plan(dtype, B, Q, N, H, l.Dp, b);
+  l.total = l.plan.total;
+  if (l.Dp == D) return l;
+  const size_t e = elem_bytes(dtype), rq = (size_t)(B * Q * H) * l.Dp, rk = (size_t)(B * N * H) * l.Dp;
+  size_t o = align256(l.total);
+  l.off_q = o; o += align256(rq * e);
+  l.off_k = o; o += align256(rk * e);
+  l.off_v = o; o += align256(rk * e);
+  l.off_out = o; o += align256(rq * e);
+  l.off_dout = o; o += align256(rq * e);
+  l.off_rc = o; o += align256(rq * 4);
+  l.off_dq = o; o += align256(rq * e);
+  l.off_dk = o; o += align256(rk * e);
+  l.off_dv = o; o += align256(rk * e);
+  l.total = o;
+  return l;
+}
+
 }  // namespace
 
 extern "C" {
 
 int st_abi_version(void) { return ST_ABI_VERSION; }
+
+size_t st_launch_report(char* buf, size_t cap) { return st::report_json(buf, cap); }
 
 const char* st_last_error(void) { return g_last_error.c_str(); }
 
@@ -94,7 +154,7 @@ size_t st_dense_fwd_workspace_bytes(int dtype, int64_t batch, int64_t queries, i
   if (check_dtype(dtype) || check_sizes(batch, queries, keys, heads, head_dim, block_size) ||
       check_envelope(head_dim, block_size))
     return 0;
-  return st::dense_fwd_plan(dtype, batch, queries, keys, heads, head_dim).total;
+  return dense_fwd_layout(dtype, batch, queries, keys, heads, head_dim).total;
 }
 
 int st_dense_fwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_t heads,
@@ -107,16 +167,30 @@ int st_dense_fwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_
     return e;
   if (!q || !k || !v || !positions || !out || !rc || !pr || !zr || !z)
     return fail(ST_EINVAL, "st_dense_fwd: null pointer argument");
-  const st::DenseFwdPlan plan = st::dense_fwd_plan(dtype, batch, queries, keys, heads, head_dim);
-  if (workspace_bytes < plan.total || (plan.total && !workspace))
-    return fail(ST_EINVAL, "st_dense_fwd: workspace of %zu bytes, %zu needed", workspace_bytes, plan.total);
+  const FwdLayout lay = dense_fwd_layout(dtype, batch, queries, keys, heads, head_dim);
+  const st::DenseFwdPlan& plan = lay.plan;
+  if (workspace_bytes < lay.total || (lay.total && !workspace))
+    return fail(ST_EINVAL, "st_dense_fwd: workspace of %zu bytes, %zu needed", workspace_bytes, lay.total);
   if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
     return fail(ST_EINVAL, "st_dense_fwd: workspace must be 256-byte aligned");
+  hipStream_t s = as_stream(stream);
+  char* ws = reinterpret_cast<char*>(workspace);
+  const bool padded = lay.Dp != head_dim;
+  const int D = (int)head_dim, Dp = (int)lay.Dp, eb = (int)elem_bytes(dtype);
+  const int64_t rq = batch * queries * heads, rk = batch * keys * heads;
   st::DenseArgs a = {};
   a.q = q; a.k = k; a.v = v; a.pos = positions;
   a.out = out; a.rc = rc; a.pr = pr; a.zr = zr; a.z = z;
+  if (padded) {
+    hipError_t he;
+    if ((he = st::launch_pad_rows(eb, ws + lay.off_q, q, rq, D, Dp, false, s)) != hipSuccess ||
+        (he = st::launch_pad_rows(eb, ws + lay.off_k, k, rk, D, Dp, false, s)) != hipSuccess ||
+        (he = st::launch_pad_rows(eb, ws + lay.off_v, v, rk, D, Dp, false, s)) != hipSuccess)
+      return launched(he, "st_dense_fwd (pad)");
+    a.q = ws + lay.off_q; a.k = ws + lay.off_k; a.v = ws + lay.off_v;
+    a.out = ws + lay.off_out; a.rc = reinterpret_cast<float*>(ws + lay.off_rc);
+  }
   if (plan.total) {
-    char* ws = reinterpret_cast<char*>(workspace);
     a.fw0 = reinterpret_cast<float*>(ws);
     a.fw1 = reinterpret_cast<float*>(ws + plan.off_w1);
     a.fstat = reinterpret_cast<float*>(ws + plan.off_stat);
@@ -124,11 +198,16 @@ int st_dense_fwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_
     // a row tile longer than half the longest possible one runs as two pieces
     a.f_split = (int)((keys + 127) / 128 + 1) / 2;
   }
-  a.B = (int)batch; a.Q = (int)queries; a.N = (int)keys; a.H = (int)heads; a.D = (int)head_dim;
+  a.B = (int)batch; a.Q = (int)queries; a.N = (int)keys; a.H = (int)heads; a.D = Dp;
   a.block = (int)block_size; a.logb = log2i(block_size);
   a.scale = 1.f / sqrtf((float)head_dim);
   a.scale_log2 = a.scale * 1.4426950408889634f;
-  return launched(st::launch_dense_fwd(dtype, a, as_stream(stream)), "st_dense_fwd");
+  hipError_t he = st::launch_dense_fwd(dtype, a, s);
+  if (he != hipSuccess || !padded) return launched(he, "st_dense_fwd");
+  if ((he = st::launch_pad_rows(eb, out, a.out, rq, D, Dp, true, s)) != hipSuccess ||
+      (he = st::launch_pad_rows(4, rc, a.rc, rq, D, Dp, true, s)) != hipSuccess)
+    return launched(he, "st_dense_fwd (unpad)");
+  return ok();
 }
 
 size_t st_dense_bwd_workspace_bytes(int dtype, int64_t batch, int64_t queries, int64_t keys,
@@ -136,7 +215,7 @@ size_t st_dense_bwd_workspace_bytes(int dtype, int64_t batch, int64_t queries, i
   if (check_dtype(dtype) || check_sizes(batch, queries, keys, heads, head_dim, block_size) ||
       check_envelope(head_dim, block_size))
     return 0;
-  return st::dense_bwd_plan(dtype, batch, queries, keys, heads, head_dim, block_size).total;
+  return dense_bwd_layout(dtype, batch, queries, keys, heads, head_dim, block_size).total;
 }
 
 int st_dense_bwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_t heads,
@@ -151,18 +230,36 @@ int st_dense_bwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_
   if (!q || !k || !v || !positions || !out || !rc || !pr || !zr || !z || !dout || !dq || !dk || !dv ||
       !workspace)
     return fail(ST_EINVAL, "st_dense_bwd: null pointer argument");
-  const st::DenseBwdPlan plan = st::dense_bwd_plan(dtype, batch, queries, keys, heads, head_dim, block_size);
-  const size_t need = plan.total;
-  if (workspace_bytes < need)
-    return fail(ST_EINVAL, "st_dense_bwd: workspace of %zu bytes, %zu needed", workspace_bytes, need);
+  const BwdLayout lay = dense_bwd_layout(dtype, batch, queries, keys, heads, head_dim, block_size);
+  const st::DenseBwdPlan& plan = lay.plan;
+  if (workspace_bytes < lay.total)
+    return fail(ST_EINVAL, "st_dense_bwd: workspace of %zu bytes, %zu needed", workspace_bytes, lay.total);
   if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
     return fail(ST_EINVAL, "st_dense_bwd: workspace must be 256-byte aligned");
+  hipStream_t s = as_stream(stream);
+  char* ws = reinterpret_cast<char*>(workspace);
+  const bool padded = lay.Dp != head_dim;
+  const int D = (int)head_dim, Dp = (int)lay.Dp, eb = (int)elem_bytes(dtype);
+  const int64_t rq = batch * queries * heads, rk = batch * keys * heads;
   st::DenseArgs a = {};
   a.q = q; a.k = k; a.v = v; a.pos = positions; a.dout = dout;
   a.out = const_cast<void*>(out);
   a.rc = const_cast<float*>(rc); a.pr = const_cast<float*>(pr);
   a.zr = const_cast<float*>(zr); a.z = const_cast<float*>(z);
-  char* ws = reinterpret_cast<char*>(workspace);
+  a.dq = dq; a.dk = dk; a.dv = dv;
+  if (padded) {
+    hipError_t he;
+    if ((he = st::launch_pad_rows(eb, ws + lay.off_q, q, rq, D, Dp, false, s)) != hipSuccess ||
+        (he = st::launch_pad_rows(eb, ws + lay.off_k, k, rk, D, Dp, false, s)) != hipSuccess ||
+        (he = st::launch_pad_rows(eb, ws + lay.off_v, v, rk, D, Dp, false, s)) != hipSuccess ||
+        (he = st::launch_pad_rows(eb, ws + lay.off_out, out, rq, D, Dp, false, s)) != hipSuccess ||
+        (he = st::launch_pad_rows(eb, ws + lay.off_dout, dout, rq, D, Dp, false, s)) != hipSuccess ||
+        (he = st::launch_pad_rows(4, ws + lay.off_rc, rc, rq, D, Dp, false, s)) != hipSuccess)
+      return launched(he, "st_dense_bwd (pad)");
+    a.q = ws + lay.off_q; a.k = ws + lay.off_k; a.v = ws + lay.off_v;
+    a.out = ws + lay.off_out; a.dout = ws + lay.off_dout; a.rc = reinterpret_cast<float*>(ws + lay.off_rc);
+    a.dq = ws + lay.off_dq; a.dk = ws + lay.off_dk; a.dv = ws + lay.off_dv;
+  }
   a.delta = reinterpret_cast<float*>(ws);
   a.rho = reinterpret_cast<float*>(ws + plan.off_rho);
   if (plan.fast) {
@@ -180,12 +277,17 @@ int st_dense_bwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_
     a.Qp = plan.Qp;
     a.nblk = plan.nblk;
   }
-  a.dq = dq; a.dk = dk; a.dv = dv;
-  a.B = (int)batch; a.Q = (int)queries; a.N = (int)keys; a.H = (int)heads; a.D = (int)head_dim;
+  a.B = (int)batch; a.Q = (int)queries; a.N = (int)keys; a.H = (int)heads; a.D = Dp;
   a.block = (int)block_size; a.logb = log2i(block_size);
   a.scale = 1.f / sqrtf((float)head_dim);
   a.scale_log2 = a.scale * 1.4426950408889634f;
-  return launched(st::launch_dense_bwd(dtype, a, as_stream(stream)), "st_dense_bwd");
+  hipError_t he = st::launch_dense_bwd(dtype, a, s);
+  if (he != hipSuccess || !padded) return launched(he, "st_dense_bwd");
+  if ((he = st::launch_pad_rows(eb, dq, a.dq, rq, D, Dp, true, s)) != hipSuccess ||
+      (he = st::launch_pad_rows(eb, dk, a.dk, rk, D, Dp, true, s)) != hipSuccess ||
+      (he = st::launch_pad_rows(eb, dv, a.dv, rk, D, Dp, true, s)) != hipSuccess)
+    return launched(he, "st_dense_bwd (unpad)");
+  return ok();
 }
 
 // ---------------------------------------------------------------------------
@@ -271,8 +373,10 @@ int st_sparse_pop(int dtype, int64_t batch, int64_t queries, int64_t heads, int6
                   const void* v, const int32_t* page_table, int64_t page_tokens,
                   int64_t pages_per_seq, int64_t n_tokens, int64_t token_offset,
                   const int64_t* ids, const float* top_scores, const float* log_zr, int64_t topk,
-                  void* out, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+                  int out_dtype, void* out, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
   int e;
+  if (out_dtype != dtype && out_dtype != ST_DTYPE_F32)
+    return fail(ST_EINVAL, "st_sparse_pop: out_dtype must be the input dtype or ST_DTYPE_F32");
   if ((e = check_dtype(dtype)) || (e = check_sizes(batch, queries, 1, heads, head_dim, block_size)) ||
       (e = check_envelope(head_dim, block_size)) ||
       (e = check_kv("st_sparse_pop", block_size, k, page_table, page_tokens, pages_per_seq, n_tokens,
@@ -295,6 +399,7 @@ int st_sparse_pop(int dtype, int64_t batch, int64_t queries, int64_t heads, int6
   a.log_zr = const_cast<float*>(log_zr);
   a.topk = (int)topk;
   a.out = out;
+  a.out_f32 = out_dtype == ST_DTYPE_F32 && dtype != ST_DTYPE_F32;
   a.lse = lse;
   a.partial = reinterpret_cast<float*>(workspace);
   return launched(st::launch_sparse_pop(dtype, a, as_stream(stream)), "st_sparse_pop");

@@ -80,6 +80,11 @@ template <> struct Mma16<f16> {
   }
 };
 
+// ST_DTYPE_* code of an element type (launch records).
+template <typename T> constexpr int dtype_code() {
+  return sizeof(T) == 4 ? 0 : (__is_same(T, f16) ? 1 : 2);
+}
+
 template <typename T> __device__ __forceinline__ T from_float(float x) { return (T)x; }
 // fp32 -> fp16 keeps the value in a full VGPR first: otherwise hipcc folds
 // the fma/mul that produced it into v_fma_mix{lo,hi}_f16, and fragments built

@@ -13,6 +13,7 @@
 // One exp per score element; exp(a_i - s_j) = u_i / U_j and
 // exp(a_i - log Z_R) = u_i come from the same u.
 #include "dense.h"
+#include "report.h"
 #include "tile.h"
 
 namespace st {
@@ -443,14 +444,20 @@ template <typename T, int DP, int NT>
 static hipError_t launch_bwd(const DenseArgs& a, hipStream_t stream) {
   constexpr int WAVES = 4;
   const int64_t rows = (int64_t)a.B * a.Q * a.H;
+  note_launch((const void*)&dense_bwd_pre_kernel<T>,
+              {"dense_bwd_pre", dtype_code<T>(), a.D, a.block, 4, a.D, 4, 0, (unsigned)((rows + 3) / 4), "rows"});
   hipLaunchKernelGGL((dense_bwd_pre_kernel<T>), dim3((rows + 3) / 4), dim3(256), 0, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   dim3 gq((a.Q + 32 * WAVES - 1) / (32 * WAVES), a.B * a.H);
+  note_launch((const void*)&dense_bwd_dq_kernel<T, DP, NT, WAVES>,
+              {"dense_bwd_dq", dtype_code<T>(), DP, a.block, 32 * WAVES, NT, WAVES, 1, gq.x * gq.y * gq.z, "grid"});
   hipLaunchKernelGGL((dense_bwd_dq_kernel<T, DP, NT, WAVES>), gq, dim3(WAVES * 64), 0, stream, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   dim3 gk((a.N + 127) / 128, a.B * a.H);
+  note_launch((const void*)&dense_bwd_dkv_kernel<T, DP>,
+              {"dense_bwd_dkv", dtype_code<T>(), DP, a.block, 128, 32, 4, 1, gk.x * gk.y * gk.z, "grid"});
   hipLaunchKernelGGL((dense_bwd_dkv_kernel<T, DP>), gk, dim3(256), 0, stream, a);
   return hipGetLastError();
 }

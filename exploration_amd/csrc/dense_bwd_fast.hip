@@ -30,6 +30,7 @@
 // come from ds_read_tr16_b64. Workgroups are numbered head-fastest, so the
 // dispatcher's round-robin over the XCDs keeps one head per XCD L2.
 #include "dense.h"
+#include "report.h"
 #include "tile.h"
 
 namespace st {
@@ -878,11 +879,23 @@ static hipError_t launch_fast(const DenseArgs& args, hipStream_t stream) {
   const int n_lim = (n_rows + 255) / 256;
   const int64_t pairs = (int64_t)a.B * a.Q * a.H;
   const int n_pre = (int)((pairs + 256 / (DP / 8) - 1) / (256 / (DP / 8)));
+  note_launch((const void*)&dense_bwd_prep_kernel<T, DP>,
+              {"dense_bwd_prep", dtype_code<T>(), DP, a.block, 256 / (DP / 8), DP, 4, 0, (unsigned)(n_lim + n_pre),
+               "rows"});
   hipLaunchKernelGGL((dense_bwd_prep_kernel<T, DP>), dim3(n_lim + n_pre), dim3(256), 0, stream, a, n_lim,
                      (int)(n_qtiles * BH), (int)(n_ktiles * BH));
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   auto go = [&]<int LOGB>() {
+    note_launch((const void*)&dense_bwd_dq_fast_kernel<T, DP, LOGB>,
+                {"dense_bwd_dq_fast", dtype_code<T>(), DP, 1 << LOGB, 128, 128, 4, 2, q_slots * BH,
+                 a.q_pair ? "pair" : "slot"});
+    note_launch((const void*)&dense_bwd_dkv_fast_kernel<T, DP, LOGB>,
+                {"dense_bwd_dkv_fast", dtype_code<T>(), DP, 1 << LOGB, 128, 64, 4, 2, k_slots * BH,
+                 a.k_pair ? "pair" : "slot"});
+    note_launch((const void*)&dense_bwd_merge_kernel<T, DP>,
+                {"dense_bwd_merge", dtype_code<T>(), DP, 1 << LOGB, 128, DP, 4, 0,
+                 (unsigned)((n_qtiles + n_ktiles) * BH * 2 * (DP / 32)), "rows"});
     hipLaunchKernelGGL((dense_bwd_dq_fast_kernel<T, DP, LOGB>), dim3(q_slots * BH), dim3(256), 0, stream,
                        a, n_qtiles);
     if (hipPeekAtLastError() != hipSuccess) return;

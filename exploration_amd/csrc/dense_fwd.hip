@@ -16,6 +16,7 @@
 // remote mean value is acc / dr. The mean is parked in RC, then a local pass
 // (plain online softmax over the window) reuses the accumulator registers.
 #include "dense.h"
+#include "report.h"
 #include "tile.h"
 
 namespace st {
@@ -260,6 +261,8 @@ template <typename T, int DP, int NT>
 static hipError_t launch_fwd(const DenseArgs& a, hipStream_t stream) {
   constexpr int WAVES = 4;
   dim3 grid((a.Q + 32 * WAVES - 1) / (32 * WAVES), a.B * a.H);
+  note_launch((const void*)&dense_fwd_kernel<T, DP, NT, WAVES>,
+              {"dense_fwd", dtype_code<T>(), DP, a.block, 32 * WAVES, NT, WAVES, 1, grid.x * grid.y * grid.z, "grid"});
   hipLaunchKernelGGL((dense_fwd_kernel<T, DP, NT, WAVES>), grid, dim3(WAVES * 64), 0, stream, a);
   return hipGetLastError();
 }

@@ -13,6 +13,7 @@
 #include <utility>
 
 #include "dense.h"
+#include "report.h"
 #include "tile.h"
 
 namespace st {
@@ -681,6 +682,9 @@ static hipError_t launch_fast(const DenseArgs& args, hipStream_t stream) {
   const int per_head = a.f_pair ? 3 * (n_qtiles / 2) + (n_qtiles & 1) : a.fw0 != nullptr ? 2 * n_qtiles : n_qtiles;
   dim3 grid((unsigned)(per_head * a.B * a.H));
   auto go = [&]<int LOGB>() {
+    note_launch((const void*)&dense_fwd_fast_kernel<T, DP, LOGB>,
+                {"dense_fwd_fast", dtype_code<T>(), DP, 1 << LOGB, 128, 128, 4, 2, grid.x,
+                 a.f_pair ? "pair" : (a.fw0 ? "slot" : "grid")});
     hipLaunchKernelGGL((dense_fwd_fast_kernel<T, DP, LOGB>), grid, dim3(256), 0, stream, a, n_qtiles);
   };
   switch (a.logb) {
@@ -695,6 +699,8 @@ static hipError_t launch_fast(const DenseArgs& args, hipStream_t stream) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.fw0 == nullptr) return e;
   constexpr int WPI = 128 / (256 / (DP / 8));
+  note_launch((const void*)&dense_fwd_merge_kernel<T, DP>,
+              {"dense_fwd_merge", dtype_code<T>(), DP, a.block, 256 / (DP / 8), DP, 4, 0, items * WPI, "rows"});
   hipLaunchKernelGGL((dense_fwd_merge_kernel<T, DP>), dim3(items * WPI), dim3(256), 0, stream, a, n_qtiles);
   return hipGetLastError();
 }

@@ -28,6 +28,7 @@
 // chunk: its dq is zero.
 #include "common.h"
 #include "halo.h"
+#include "report.h"
 #include "tile.h"
 
 namespace st {
@@ -1028,15 +1029,33 @@ template <typename T, bool BWD>
 hipError_t dispatch(const HaloArgs& a, hipStream_t s) {
   const unsigned units = (unsigned)((int64_t)a.B * (BWD ? a.G + 1 : a.G) * a.H);
   auto go = [&]<int B_, int HD>() {
+    auto note = [&](const void* f, const char* name) {
+      note_launch(f, {name, dtype_code<T>(), HD, B_, B_, 2 * B_, 1, 1, units, "unit"});
+    };
     if constexpr (HD == 64 && B_ == 16 && sizeof(T) == 2) {
-      if constexpr (BWD) hipLaunchKernelGGL((halo_bwd_mfma_kernel<T>), dim3(units), dim3(64), 0, s, a);
-      else hipLaunchKernelGGL((halo_fwd_mfma_kernel<T>), dim3(units), dim3(64), 0, s, a);
+      if constexpr (BWD) {
+        note((const void*)&halo_bwd_mfma_kernel<T>, "halo_bwd_mfma");
+        hipLaunchKernelGGL((halo_bwd_mfma_kernel<T>), dim3(units), dim3(64), 0, s, a);
+      } else {
+        note((const void*)&halo_fwd_mfma_kernel<T>, "halo_fwd_mfma");
+        hipLaunchKernelGGL((halo_fwd_mfma_kernel<T>), dim3(units), dim3(64), 0, s, a);
+      }
     } else if constexpr (HD == 64) {
-      if constexpr (BWD) hipLaunchKernelGGL((halo_bwd64_kernel<T, B_>), dim3(units), dim3(64), 0, s, a);
-      else hipLaunchKernelGGL((halo_fwd64_kernel<T, B_>), dim3(units), dim3(64), 0, s, a);
+      if constexpr (BWD) {
+        note((const void*)&halo_bwd64_kernel<T, B_>, "halo_bwd64");
+        hipLaunchKernelGGL((halo_bwd64_kernel<T, B_>), dim3(units), dim3(64), 0, s, a);
+      } else {
+        note((const void*)&halo_fwd64_kernel<T, B_>, "halo_fwd64");
+        hipLaunchKernelGGL((halo_fwd64_kernel<T, B_>), dim3(units), dim3(64), 0, s, a);
+      }
     } else {
-      if constexpr (BWD) hipLaunchKernelGGL((halo_bwd_kernel<T, B_, HD>), dim3(units), dim3(64), 0, s, a);
-      else hipLaunchKernelGGL((halo_fwd_kernel<T, B_, HD>), dim3(units), dim3(64), 0, s, a);
+      if constexpr (BWD) {
+        note((const void*)&halo_bwd_kernel<T, B_, HD>, "halo_bwd");
+        hipLaunchKernelGGL((halo_bwd_kernel<T, B_, HD>), dim3(units), dim3(64), 0, s, a);
+      } else {
+        note((const void*)&halo_fwd_kernel<T, B_, HD>, "halo_fwd");
+        hipLaunchKernelGGL((halo_fwd_kernel<T, B_, HD>), dim3(units), dim3(64), 0, s, a);
+      }
     }
     return hipGetLastError();
   };

@@ -26,7 +26,7 @@ struct SparseArgs {
   int64_t* ids;            // [B,Q,H,topk]
   float* top_scores;       // [B,Q,H,topk]
   float* log_zr;           // [B,Q,H]
-  void* out;               // [B,Q,H,D] in the input dtype
+  void* out;               // [B,Q,H,D] in the input dtype (float if out_f32)
   float* lse;              // [B,Q,H] or nullptr
   float* partial;          // pop partials [B*Q*H, n_chunks, DP + 2]
   int B, Q, H, D;
@@ -35,6 +35,7 @@ struct SparseArgs {
   int64_t n_blocks;        // blocks of the KV range (first = token_offset / block)
   int64_t id_base;         // global id of block 0 of the scores array
   float scale_log2;        // log2(e)/sqrt(D)
+  int out_f32;             // write out as float instead of the input dtype
 };
 
 // Pop partial layout helpers shared by the ABI and the kernels.

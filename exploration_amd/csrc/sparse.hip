@@ -16,6 +16,7 @@
 //   select on the 64-bit key (ordered score, ~block id), then a rank sort.
 // sparse_pop: one wave per (row, block slot); online softmax over the block's
 //   tokens with coalesced 16-byte loads; sparse_merge combines the slots.
+#include "report.h"
 #include "sparse.h"
 #include "tile.h"
 
@@ -40,6 +41,18 @@ __device__ __forceinline__ const T* kv_token(const KvView& kv, const T* base, in
 
 template <bool PAGED> __device__ __forceinline__ int64_t kv_stride(int H, int D) {
   return PAGED ? (int64_t)D : (int64_t)H * D;
+}
+
+// N consecutive elements [d, d+N) of a row of D elements, zero past D. Rows
+// whose length is a multiple of N are N-aligned and take one vector load;
+// other head dimensions (not a multiple of 8) load element by element.
+template <typename T, typename F, int N>
+__device__ __forceinline__ F load_row_elems(const T* p, int d, int D) {
+  if (D % N == 0) return d < D ? *reinterpret_cast<const F*>(p + d) : F{};
+  F f;
+#pragma unroll
+  for (int e = 0; e < N; ++e) f[e] = d + e < D ? p[d + e] : T(0);
+  return f;
 }
 
 // ---------------------------------------------------------------------------
@@ -83,7 +96,8 @@ __global__ __launch_bounds__(256) void sparse_scores_kernel(SparseArgs a) {
 #pragma unroll
       for (int c = 0; c < NKC; ++c) {
         const int d = c * M::KW + half * M::VEC;
-        qf[c] = (row_in && d < a.D) ? *reinterpret_cast<const Frag*>(qrow + d) : Frag{};
+        if constexpr (M::VEC == 1) qf[c] = (row_in && d < a.D) ? qrow[d] : 0.f;
+        else qf[c] = row_in ? load_row_elems<T, Frag, M::VEC>(qrow, d, a.D) : Frag{};
       }
       f32x16 s[NST];
 #pragma unroll
@@ -95,7 +109,9 @@ __global__ __launch_bounds__(256) void sparse_scores_kernel(SparseArgs a) {
 #pragma unroll
         for (int c = 0; c < NKC; ++c) {
           const int d = c * M::KW + half * M::VEC;
-          const Frag kf = d < a.D ? *reinterpret_cast<const Frag*>(krow + d) : Frag{};
+          Frag kf;
+          if constexpr (M::VEC == 1) kf = d < a.D ? krow[d] : 0.f;
+          else kf = load_row_elems<T, Frag, M::VEC>(krow, d, a.D);
           acc = M::mma(kf, qf[c], acc);
         }
 #pragma unroll
@@ -227,7 +243,8 @@ __global__ __launch_bounds__(64, 2) void sparse_scan_kernel(SparseArgs a) {
 #pragma unroll
       for (int c = 0; c < NKC; ++c) {
         const int d = c * M::KW + half * M::VEC;
-        qf[c] = (row_in && d < a.D) ? *reinterpret_cast<const Frag*>(qrow + d) : Frag{};
+        if constexpr (M::VEC == 1) qf[c] = (row_in && d < a.D) ? qrow[d] : 0.f;
+        else qf[c] = row_in ? load_row_elems<T, Frag, M::VEC>(qrow, d, a.D) : Frag{};
       }
       wait_vm();
     }
@@ -942,8 +959,7 @@ __global__ __launch_bounds__(256) void sparse_pop_kernel(SparseArgs a) {
   float q[E];
   {
     const T* qrow = reinterpret_cast<const T*>(a.q) + row * a.D;
-    V qv = {};
-    if (e0 < a.D) qv = load_vec<V>(qrow + e0);
+    const V qv = load_row_elems<T, V, E>(qrow, e0, a.D);
 #pragma unroll
     for (int e = 0; e < E; ++e) q[e] = to_float<T>(qv[e]) * a.scale_log2;
   }
@@ -966,9 +982,9 @@ __global__ __launch_bounds__(256) void sparse_pop_kernel(SparseArgs a) {
        const int i = i00 + TPI * j + g;
        kvs[j] = V{};
        vvs[j] = V{};
-       if (i < ntok && e0 < a.D) {
-         kvs[j] = load_vec<V>(kb + (int64_t)i * stride + e0);
-         vvs[j] = load_vec<V>(vb + (int64_t)i * stride + e0);
+       if (i < ntok) {
+         kvs[j] = load_row_elems<T, V, E>(kb + (int64_t)i * stride, e0, a.D);
+         vvs[j] = load_row_elems<T, V, E>(vb + (int64_t)i * stride, e0, a.D);
        }
      }
 #pragma unroll
@@ -1037,7 +1053,7 @@ __global__ __launch_bounds__(256) void sparse_pop_kernel(SparseArgs a) {
 // kernel is bound by load latency: each lane fetches one chunk's (max, mass)
 // and the chunk outputs are read eight chunks at a time, all loads of a
 // round in flight together.
-template <typename T, int DP>
+template <typename T, int DP, typename TO = T>
 __global__ __launch_bounds__(64) void sparse_merge_kernel(SparseArgs a, int chunks) {
   constexpr int S = DP + 2;
   constexpr int NJ = DP / 64;
@@ -1080,11 +1096,11 @@ __global__ __launch_bounds__(64) void sparse_merge_kernel(SparseArgs a, int chun
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off, 64);
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  T* out = reinterpret_cast<T*>(a.out) + row * a.D;
+  TO* out = reinterpret_cast<TO*>(a.out) + row * a.D;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int d = lane + 64 * j;
-    if (d < a.D) out[d] = from_float<T>(o[j] * inv);
+    if (d < a.D) out[d] = from_float<TO>(o[j] * inv);
   }
   if (a.lse && lane == 0) a.lse[row] = (l > 0.f && mm != kNegInf) ? (mm + fast_log2(l)) * kLn2 : kNegInf;
 }
@@ -1092,13 +1108,25 @@ __global__ __launch_bounds__(64) void sparse_merge_kernel(SparseArgs a, int chun
 // ---------------------------------------------------------------------------
 template <typename T, int DP>
 static hipError_t scores_dp(const SparseArgs& a, hipStream_t s) {
+  auto note_scores = [&](const void* f, const char* name, dim3 g) {
+    note_launch(f, {name, dtype_code<T>(), DP, a.block, 128, 16, 4, 1, g.x * g.y * g.z,
+                    a.kv.page_table ? "paged" : "contiguous"});
+  };
   const int64_t chunks = (a.kv.n_tokens + 127) / 128;
   dim3 grid((unsigned)((chunks + 3) / 4), a.H, a.B);
   if constexpr (sizeof(T) == 2 && DP <= 128) {
+    if (a.D % 8 != 0) {
+      // rows that are not 16-byte multiples: the element-load kernel
+      note_scores((const void*)&sparse_scores_kernel<T, DP, true>, "sparse_scores", grid);
+      if (a.kv.page_table) hipLaunchKernelGGL((sparse_scores_kernel<T, DP, true>), grid, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((sparse_scores_kernel<T, DP, false>), grid, dim3(256), 0, s, a);
+      return hipGetLastError();
+    }
     if (a.D % 32 == 0) {
       if ((chunks + 3) / 4 * a.H >= (int64_t(1) << 31)) return hipErrorInvalidConfiguration;
       grid = dim3((unsigned)((chunks + 3) / 4 * a.H), 1, a.B);
       auto go16 = [&]<int LOGB>() {
+        note_scores((const void*)&sparse_scan16_kernel<T, DP, true, LOGB>, "sparse_scan16", grid);
         if (a.kv.page_table) hipLaunchKernelGGL((sparse_scan16_kernel<T, DP, true, LOGB>), grid, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((sparse_scan16_kernel<T, DP, false, LOGB>), grid, dim3(256), 0, s, a);
       };
@@ -1115,6 +1143,7 @@ static hipError_t scores_dp(const SparseArgs& a, hipStream_t s) {
     }
     dim3 g1((unsigned)chunks, a.H, a.B);
     auto go = [&]<int LOGB>() {
+      note_scores((const void*)&sparse_scan_kernel<T, DP, true, LOGB>, "sparse_scan", g1);
       if (a.kv.page_table) hipLaunchKernelGGL((sparse_scan_kernel<T, DP, true, LOGB>), g1, dim3(64), 0, s, a);
       else hipLaunchKernelGGL((sparse_scan_kernel<T, DP, false, LOGB>), g1, dim3(64), 0, s, a);
     };
@@ -1128,6 +1157,7 @@ static hipError_t scores_dp(const SparseArgs& a, hipStream_t s) {
       default: go.template operator()<7>(); break;
     }
   } else {
+    note_scores((const void*)&sparse_scores_kernel<T, DP, true>, "sparse_scores", grid);
     if (a.kv.page_table) hipLaunchKernelGGL((sparse_scores_kernel<T, DP, true>), grid, dim3(256), 0, s, a);
     else hipLaunchKernelGGL((sparse_scores_kernel<T, DP, false>), grid, dim3(256), 0, s, a);
   }
@@ -1152,6 +1182,14 @@ hipError_t launch_sparse_scores(int dtype, const SparseArgs& a, hipStream_t stre
 hipError_t launch_sparse_select(int64_t rows, int64_t n_blocks, int topk, int64_t id_base,
                                 const float* scores, int64_t* ids, float* top, float* log_zr,
                                 hipStream_t stream) {
+  auto note = [&](const void* f, const char* name, int threads) {
+    note_launch(f, {name, 0, 0, 0, 1, (int)(n_blocks < 0x7fffffff ? n_blocks : 0x7fffffff), threads / 64, 0,
+                    (unsigned)rows, "row"});
+  };
+  if (topk <= 64 && n_blocks <= 512 * 16) note((const void*)&sparse_select_radix_kernel<512, 16>, "sparse_select_radix", 512);
+  else if (topk <= 64 && n_blocks <= 512 * 32) note((const void*)&sparse_select_radix_kernel<512, 32>, "sparse_select_radix", 512);
+  else if (topk <= 64) note((const void*)&sparse_select64_kernel, "sparse_select64", 256);
+  else note((const void*)&sparse_select_kernel, "sparse_select", 256);
   if (topk <= 64 && n_blocks <= 512 * 16)
     hipLaunchKernelGGL((sparse_select_radix_kernel<512, 16>), dim3((unsigned)rows), dim3(512), 0, stream, n_blocks,
                        topk, id_base, scores, ids, top, log_zr);
@@ -1172,11 +1210,17 @@ static hipError_t pop_dp(const SparseArgs& a, hipStream_t s) {
   const int64_t rows = (int64_t)a.B * a.Q * a.H;
   const int chunks = (int)sparse_chunks(a.topk);
   dim3 grid((unsigned)rows, chunks);
+  note_launch((const void*)&sparse_pop_kernel<T, DP, true>,
+              {"sparse_pop", dtype_code<T>(), DP, a.block, 1, a.block, 4, 0, grid.x * grid.y,
+               a.kv.page_table ? "paged" : "contiguous"});
+  note_launch((const void*)&sparse_merge_kernel<T, DP>,
+              {"sparse_merge", dtype_code<T>(), DP, a.block, 1, DP, 1, 0, grid.x, "row"});
   if (a.kv.page_table) hipLaunchKernelGGL((sparse_pop_kernel<T, DP, true>), grid, dim3(256), 0, s, a);
   else hipLaunchKernelGGL((sparse_pop_kernel<T, DP, false>), grid, dim3(256), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((sparse_merge_kernel<T, DP>), dim3((unsigned)rows), dim3(64), 0, s, a, chunks);
+  if (a.out_f32) hipLaunchKernelGGL((sparse_merge_kernel<T, DP, float>), dim3((unsigned)rows), dim3(64), 0, s, a, chunks);
+  else hipLaunchKernelGGL((sparse_merge_kernel<T, DP>), dim3((unsigned)rows), dim3(64), 0, s, a, chunks);
   return hipGetLastError();
 }
 

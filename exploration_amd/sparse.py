@@ -228,11 +228,18 @@ def _sparse_host(q, cache, positions, b, topk, return_selection):
     _lib.check(lib.st_sparse_pop(_lib.DTYPE_CODES[q.dtype], batch, queries, heads, dim, b, _lib.ptr(q),
                                  _lib.ptr(pos), _lib.ptr(pools[0]), _lib.ptr(pools[1]), _lib.ptr(table), b,
                                  n_blocks, n, off, _lib.ptr(ids), _lib.ptr(values), _lib.ptr(log_zr), topk,
-                                 _lib.ptr(out), None, _lib.ptr(ws), ws.numel(), _lib.stream_of(q)), lib)
+                                 _lib.DTYPE_CODES[q.dtype], _lib.ptr(out), None, _lib.ptr(ws), ws.numel(),
+                                 _lib.stream_of(q)), lib)
     _record("sparse_pop", q, b, True)
     if return_selection:
         return out, {"indices": ids, "scores": values, "log_zr": log_zr}
     return out
+
+
+def _host_resident(cache):
+    k, v = getattr(cache, "k", None), getattr(cache, "v", None)
+    return (isinstance(k, torch.Tensor) and isinstance(v, torch.Tensor) and k.device.type == "cpu"
+            and v.device.type == "cpu")
 
 
 def _kv_view(cache, q, block_size):
@@ -282,6 +289,11 @@ def sparse_attention(q, cache, positions, block_size, topk, backend="auto", grou
         raise ValueError("unsupported HIP sparse configuration")
     if q.ndim != 4 or positions.shape != q.shape[:2]:
         raise ValueError("expected q[B,Q,H,D], positions[B,Q]")
+    if not isinstance(cache, (HostPages, PagedKV)) and _host_resident(cache):
+        # a TensorPages / KVCache over host memory (the reference's CPU and
+        # disk tiers, st/runtime/inference.py:19-43): streamed like HostPages
+        cache = HostPages(cache.k, cache.v, q.device, chunk_tokens=max(b, score_page_tokens // b * b),
+                          offset=cache.offset)
     if isinstance(cache, HostPages):
         return _sparse_host(q.contiguous(), cache, positions.to(device=q.device, dtype=torch.int64).contiguous(),
                             b, topk, return_selection)
@@ -309,10 +321,12 @@ def sparse_attention(q, cache, positions, block_size, topk, backend="auto", grou
 
 
 @torch.inference_mode()
-def block_scores(q, k, positions, block_size, offset=0):
+def block_scores(q, k, positions, block_size, offset=0, *, force_streamed=False):
     """Exact block scores ``[B,Q,H,G]`` (float32) of a contiguous KV slab that
     starts at absolute token ``offset`` (reference internal
-    ``st/ops/kernels/sparse.py:81-100``)."""
+    ``st/ops/kernels/sparse.py:81-100``). ``force_streamed`` picks the
+    reference's small-tile NVIDIA fallback there; one kernel family serves
+    both settings here."""
     lib = _lib.load()
     if not hip_supported(q, block_size) or k.dtype != q.dtype:
         raise ValueError("unsupported HIP block-score configuration")
@@ -348,8 +362,9 @@ def select_blocks(scores, topk, id_base=0):
 def sparse_pop(q, k, v, positions, ids, scores, log_zr, block_size, offset=0):
     """Gated softmax read of the local window and the selected blocks from a
     contiguous KV slab starting at absolute token ``offset``; returns
-    ``(out in q.dtype, lse float32)`` (reference ``st/ops/kernels/sparse.py:103-113``
-    returns the float32 partial of one page; here the read is complete)."""
+    ``(out float32, lse float32)`` as the reference does
+    (``st/ops/kernels/sparse.py:103-113``; its caller merges page partials by
+    LSE and casts to ``q.dtype``, ``st/ops/sparse.py:157-174``)."""
     lib = _lib.load()
     if not hip_supported(q, block_size):
         raise ValueError("unsupported HIP sparse configuration")
@@ -360,12 +375,12 @@ def sparse_pop(q, k, v, positions, ids, scores, log_zr, block_size, offset=0):
     topk = ids.shape[-1]
     ws_bytes = lib.st_sparse_workspace_bytes(batch, queries, heads, dim, topk, 0)
     ws = torch.empty(max(ws_bytes, 256), device=q.device, dtype=torch.uint8)
-    out = torch.empty_like(q)
+    out = torch.empty(q.shape, device=q.device, dtype=torch.float32)
     lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
     _lib.check(lib.st_sparse_pop(_lib.DTYPE_CODES[q.dtype], batch, queries, heads, dim, block_size,
                                  _lib.ptr(q), _lib.ptr(positions), _lib.ptr(k), _lib.ptr(v), None,
                                  block_size, 0, k.shape[1], offset, _lib.ptr(ids), _lib.ptr(scores),
-                                 _lib.ptr(log_zr), topk, _lib.ptr(out), _lib.ptr(lse), _lib.ptr(ws),
-                                 ws.numel(), _lib.stream_of(q)), lib)
+                                 _lib.ptr(log_zr), topk, _lib.DTYPE_CODES[torch.float32], _lib.ptr(out),
+                                 _lib.ptr(lse), _lib.ptr(ws), ws.numel(), _lib.stream_of(q)), lib)
     _record("sparse_pop", q, block_size, False)
     return out, lse

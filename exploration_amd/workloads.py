@@ -115,6 +115,37 @@ def planted_sparse(batch, heads, length, queries, dim, block, topk, page_tokens,
     return q, cache, positions, expected
 
 
+def plant_blocks(q, k, positions, block, topk, queries, generator, noise=0.05):
+    """Plant ``topk`` well-separated key blocks for the query indices
+    ``queries`` (every batch row and head) into ``k [B, N, H, D]`` in place.
+
+    Block r of query t holds keys ``alpha_r sqrt(D) q_hat_t + noise N(0,1)``
+    (strictly decreasing ``alpha_r``), chosen among the blocks visible to all
+    of ``queries`` and distinct across them within a head. Returns the
+    expected ids ``[B, len(queries), H, topk]`` in rank order."""
+    batch, _, heads, dim = q.shape
+    device = k.device
+    pos = positions[:, list(queries)]
+    n_visible = int(pos.min()) // block - 1
+    if len(queries) * topk > n_visible:
+        raise ValueError("not enough visible blocks to plant disjoint selections")
+    alphas = planted_alphas(topk).to(device)
+    qf = q.float()
+    qhat = qf / qf.norm(dim=-1, keepdim=True)
+    expected = torch.empty((batch, len(queries), heads, topk), device=device, dtype=torch.int64)
+    for bi in range(batch):
+        for h in range(heads):
+            ids = torch.randperm(n_visible, generator=generator, device=device)[:len(queries) * topk]
+            ids = ids.reshape(len(queries), topk)
+            expected[bi, :, h] = ids
+            qh = qhat[bi, list(queries), h]
+            keys = (alphas[None, :, None, None] * math.sqrt(dim) * qh[:, None, None, :]
+                    + noise * torch.randn((len(queries), topk, block, dim), generator=generator, device=device))
+            tokens = (ids[..., None] * block + torch.arange(block, device=device)).reshape(-1)
+            k[bi, tokens, h] = keys.reshape(-1, dim).to(k.dtype)
+    return expected
+
+
 def sparse_bytes(positions, ids, heads, dim, block, elem_bytes):
     """Algorithmic HBM bytes of one sparse forward: every visible key block is
     read once per (batch, head) by the scan, then the keys and values of the

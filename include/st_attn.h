@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ST_ABI_VERSION 3
+#define ST_ABI_VERSION 4
 
 #define ST_DTYPE_F32 0
 #define ST_DTYPE_F16 1
@@ -50,17 +50,32 @@ int st_abi_version(void);
 /* Message of the last failing call on this thread ("" if none). */
 const char* st_last_error(void);
 
+/* Launch records as a JSON array, one object per (kernel, device, dtype,
+ * head_dim, block_size, mode) launched so far: the reference's report
+ * fields (st/ops/kernels/launch.py:52-56,96-98: kernel, path, device, dtype,
+ * head_dim, block_size, tile_m, tile_n, num_warps = waves per workgroup,
+ * num_stages = LDS buffers per operand, shared_memory_bytes) plus vgprs,
+ * scratch_bytes, workgroups and mode. Writes at most cap bytes (NUL
+ * terminated) and returns the size the whole report needs. */
+size_t st_launch_report(char* buf, size_t cap);
+
 /* 1 if the fused kernels support (dtype, head_dim, block_size), else 0.
  * Replaces the Triton capability predicate triton_supported
  * (st/ops/attention.py:142-145): fp32/fp16/bf16, block a power of two in
- * [2, 128], head_dim <= 256 (here also a multiple of 8). */
+ * [2, 128], head_dim <= 256. The reference pads D to a power of two inside
+ * its kernel (st/ops/kernels/dense.py:210); here a head_dim that is not a
+ * multiple of 8 runs the dense kernels on zero-padded copies held in the
+ * workspace (its size includes them) and the sparse kernels with element
+ * loads. */
 int st_dense_supported(int dtype, int64_t head_dim, int64_t block_size);
 
 /* Bytes of device workspace st_dense_fwd needs for this problem (0 if none
  * or if the arguments are invalid). The pipelined 16-bit path (head_dim 64
  * or 128) runs the longest causal row tiles as two pieces and merges their
  * partial results: per 128-row tile 2 x 128 x head_dim floats of partial
- * means, 128 x 8 floats of statistics and a flag. No reference counterpart:
+ * means, 128 x 8 floats of statistics and a flag. A head_dim that is not a
+ * multiple of 8 adds padded copies of q, k, v, out and rc. No reference
+ * counterpart:
  * the reference's Triton forward allocates its own buffers
  * (st/ops/kernels/dense.py:200-203). */
 size_t st_dense_fwd_workspace_bytes(int dtype, int64_t batch, int64_t queries, int64_t keys,
@@ -124,13 +139,16 @@ size_t st_sparse_workspace_bytes(int64_t batch, int64_t queries, int64_t heads, 
 /* Softmax read over the local window and the selected blocks, gated by
  * log_zr. Replaces sparse_pop / `_pop` and the LSE merge of
  * st/ops/kernels/sparse.py:38-78,103-113 and st/ops/sparse.py:157-162.
- * Writes out (dtype) and, if lse != NULL, the row logsumexp (float). */
+ * Writes out in out_dtype (`dtype`, or ST_DTYPE_F32 for the reference's
+ * float32 partial, st/ops/kernels/sparse.py:108) and, if lse != NULL, the
+ * row logsumexp (float). */
 int st_sparse_pop(int dtype, int64_t batch, int64_t queries, int64_t heads, int64_t head_dim,
                   int64_t block_size, const void* q, const int64_t* positions, const void* k,
                   const void* v, const int32_t* page_table, int64_t page_tokens,
                   int64_t pages_per_seq, int64_t n_tokens, int64_t token_offset,
                   const int64_t* ids, const float* top_scores, const float* log_zr, int64_t topk,
-                  void* out, float* lse, void* workspace, size_t workspace_bytes, void* stream);
+                  int out_dtype, void* out, float* lse, void* workspace, size_t workspace_bytes,
+                  void* stream);
 
 /* Whole sparse forward: scores, selection and read in one call
  * (st/ops/sparse.py:99-174 on one device). ids/top_scores/log_zr receive

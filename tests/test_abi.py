@@ -30,7 +30,8 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in declared_functions():
         assert hasattr(lib, name), f"{name} missing from libst_attn.so"
-    assert lib.st_abi_version() == 3
+    assert lib.st_abi_version() == 4
+    assert lib.st_launch_report(None, 0) >= 3  # "[]" and its NUL at least
     assert lib.st_last_error() == b""
 
 
@@ -42,7 +43,9 @@ def test_support_predicate():
         assert lib.st_dense_supported(dtype, 128, 3) == 0
         assert lib.st_dense_supported(dtype, 128, 256) == 0
         assert lib.st_dense_supported(dtype, 264, 64) == 0
-        assert lib.st_dense_supported(dtype, 6, 64) == 0
+        assert lib.st_dense_supported(dtype, 6, 64) == 1  # padded to 8
+        assert lib.st_dense_supported(dtype, 256, 64) == 1
+        assert lib.st_dense_supported(dtype, 0, 64) == 0
     assert lib.st_dense_supported(7, 64, 64) == 0
 
 
@@ -77,6 +80,16 @@ def test_argument_errors_map_to_value_error():
     assert lib.st_dense_bwd_workspace_bytes(2, 2, 5, 7, 3, 64, 4) == (2 * 256 + 512 + 2 * 256 + table + 2 * 256
                                                                        + partials)
     assert lib.st_dense_bwd_workspace_bytes(2, 2, 5, 7, 3, 64, 3) == 0
+    # head_dim 60 runs at 64 on padded copies: the same kernel workspace plus
+    # q, k, v, out, dout (bf16), rc (fp32) and dq, dk, dv, each 256-aligned
+    pad = lambda n: (n + 255) // 256 * 256
+    rq, rk = 2 * 5 * 3 * 64, 2 * 7 * 3 * 64
+    inner = lib.st_dense_bwd_workspace_bytes(2, 2, 5, 7, 3, 64, 4)
+    assert lib.st_dense_bwd_workspace_bytes(2, 2, 5, 7, 3, 60, 4) == (
+        pad(inner) + 4 * pad(rq * 2) + 4 * pad(rk * 2) + pad(rq * 4))
+    # fp32 head_dim 17 (generic kernels, no workspace of their own) at 24:
+    # q, k, v, out and rc copies
+    assert lib.st_dense_fwd_workspace_bytes(0, 1, 3, 3, 1, 17, 4) == 5 * pad(3 * 24 * 4)
 
 
 def test_python_entry_points_validate_like_the_reference():

@@ -13,7 +13,7 @@ import torch
 
 from exploration_amd import _lib, dense_attention, launch_report
 from exploration_amd.attention import dense_forward_stats
-from exploration_amd.workloads import CFG2, CFG3, dense_config
+from exploration_amd.workloads import CFG1, CFG2, CFG3, dense_config
 from oracle import dense as od
 from tests.helpers import assert_close, error_metrics
 
@@ -66,6 +66,34 @@ def test_validation_matrix(device, n, b, d, dtype):
     print(f"dense case n={n} b={b} d={d} {dtype}", flush=True)
     q, k, v, pos, probe = _validate_case(n, b, d, dtype)
     _check_dense(q, k, v, pos, probe, b, device, dtype, label=f"n={n} b={b} d={d}")
+
+
+def test_cfg1_fp32_causal(device):
+    """cfg1: fp32, B2 H4, N=Q=512 (positions arange), D=64, b=64, q/k/v/dO ~
+    N(0,1) from seed 0 (the reference's CPU benchmark shape,
+    st/tools/benchmark.py:27-43): forward, statistics and gradients against
+    the float64 oracle."""
+    print("dense cfg1", flush=True)
+    q, k, v, pos, do, b = dense_config(CFG1)
+    assert pos.shape == (2, 512) and pos[1].tolist() == list(range(512))
+    _check_dense(q, k, v, pos, do, b, device, torch.float32, label="cfg1")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("d", [40, 200, 20, 33, 130])
+def test_head_dim_envelope(device, d, dtype):
+    """Any head_dim up to 256 (the reference pads D inside its kernel,
+    st/ops/kernels/dense.py:210): multiples of 8 run directly, others through
+    zero-padded copies in the workspace; the scale stays 1/sqrt(head_dim)."""
+    print(f"dense head_dim {d} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(40 + d)
+    n, b = 300, 32
+    q = torch.randn(2, 70, 2, d, generator=g).to(dtype)
+    k = torch.randn(2, n, 2, d, generator=g).to(dtype)
+    v = torch.randn(2, n, 2, d, generator=g).to(dtype)
+    probe = torch.randn(2, 70, 2, d, generator=g).to(dtype)
+    pos = torch.randint(-1, n, (2, 70), generator=g)
+    _check_dense(q, k, v, pos, probe, b, device, dtype, label=f"d={d}")
 
 
 def test_cfg3_fp32_ragged_tail(device):
@@ -170,7 +198,10 @@ def test_native_library_is_the_path(device):
     out = dense_attention(q, q, q, torch.arange(8, device=device)[None], 4)
     torch.cuda.synchronize()
     assert out.shape == q.shape
-    assert any(r["kernel"] == "dense_fwd" and r["path"] == "hip" for r in launch_report())
+    report = launch_report()
+    assert any(r["kernel"] == "dense_fwd" and r["path"] == "hip" for r in report)
+    native = [r for r in report if r["kernel"].startswith("dense_fwd") and "tile_m" in r]
+    assert native and all(r["vgprs"] > 0 and r["workgroups"] > 0 for r in native), native
     runtimes = _lib.hip_runtimes_mapped()
     assert len(runtimes) == 1, runtimes
     maps = open("/proc/self/maps").read()

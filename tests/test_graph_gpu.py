@@ -77,9 +77,45 @@ def test_graphed_step_matches_eager_full_width(device):
             losses = [train_step(m, opt, ids, targets, width=8192, autocast_cache=False)[0].item() for _ in range(7)]
         else:
             step = GraphedStep(m, opt, ids, targets, warmup=1)
-            losses = [None] + [step(ids, targets)[0].item() for _ in range(6)]
+            print(f"  captured nodes {step.node_types}", flush=True)
+            assert set(step.node_types) <= {"kernel", "memcpy", "empty", "event_record", "wait_event"}
+            # six replays queued back to back, read afterwards
+            out = [step(ids, targets)[0].clone() for _ in range(6)]
+            losses = [None] + [x.item() for x in out]
         runs[mode] = (losses, [p.detach().clone() for p in m.parameters()])
         print(f"  {mode}: {losses}", flush=True)
     assert runs["graph"][0][1:] == runs["eager"][0][1:]
     for pe, pg in zip(runs["eager"][1], runs["graph"][1]):
         assert torch.equal(pe, pg)
+
+
+def test_graphed_step_skips_empty_and_nonfinite_batches(device):
+    """A replay whose batch has no supervised token (0/0 loss) leaves every
+    parameter and optimizer moment unchanged on the device (fused AdamW's
+    found_inf), and the next replay trains normally; the eager path raises
+    before backward, as the reference does (st/runtime/engine.py:170-177)."""
+    print("graphed step skip on empty batch", flush=True)
+    torch.manual_seed(0)
+    cfg = {"vocab_size": 64, "dim": 64, "heads": 2, "block_size": 16, "topk": 64, "arch": "Lx1,G",
+           "ffn_ratio": 2.0}
+    m = M.build_model(cfg, execution={"checkpoint_chunks": True, "encoder_chunk": 128}, device=device)
+    opt = make_optimizer(m, capturable=True)
+    ids, targets = synthetic_lm_batch(64, 256, batch=1, seed=1, device=device)
+    step = GraphedStep(m, opt, ids, targets, warmup=1)
+    before = [p.detach().clone() for p in m.parameters()]
+    moments = [opt.state[p]["exp_avg"].clone() for p in m.parameters()]
+    steps = [opt.state[p]["step"].clone() for p in m.parameters()]
+    empty = torch.full_like(targets, -100)
+    loss, norm, count = step(ids, empty)
+    torch.cuda.synchronize()
+    assert int(count) == 0 and not bool(torch.isfinite(loss))
+    for p, b, mo, st in zip(m.parameters(), before, moments, steps):
+        assert torch.equal(p, b)
+        assert torch.equal(opt.state[p]["exp_avg"], mo)
+        assert torch.equal(opt.state[p]["step"], st)
+    loss, _, count = step(ids, targets)
+    torch.cuda.synchronize()
+    assert int(count) == 255 and bool(torch.isfinite(loss))
+    assert any(not torch.equal(p, b) for p, b in zip(m.parameters(), before))
+    with pytest.raises(ValueError, match="no supervised tokens"):
+        train_step(m, opt, ids, empty)

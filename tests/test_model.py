@@ -237,3 +237,31 @@ def test_feedforward_matches_sequential():
     params = [f[0].weight, f[0].bias, f[2].weight, f[2].bias, x]
     for a, b in zip(torch.autograd.grad(y.sum(), params), torch.autograd.grad(ref.sum(), params)):
         torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-12)
+
+
+def test_eager_step_guards_run_before_backward(monkeypatch):
+    """Without ``width`` the step applies the reference's host guards before
+    backward (st/runtime/engine.py:170-177): an empty batch raises
+    ValueError, a non-finite loss FloatingPointError, and in both cases no
+    gradient is written and the optimizer never steps."""
+    from exploration_amd.train import make_optimizer, train_step
+
+    torch.manual_seed(0)
+    cfg = {"vocab_size": 64, "dim": 64, "heads": 2, "block_size": 16, "topk": 64, "arch": "Lx1,G", "ffn_ratio": 2.0}
+    m = M.build_model(cfg, execution={"checkpoint_chunks": False, "encoder_chunk": 128})
+    monkeypatch.setattr(M, "dense_attention", lambda q, k, v, pos, b, backend, **kw: q * 1.0)
+    opt = make_optimizer(m)
+    ids = torch.randint(64, (1, 64))
+    targets = torch.roll(ids, -1, 1)
+    before = [p.detach().clone() for p in m.parameters()]
+    with pytest.raises(ValueError, match="no supervised tokens"):
+        train_step(m, opt, ids, torch.full_like(targets, -100), precision="fp32")
+    with torch.no_grad():
+        m.lm_head.weight[0, 0] = float("nan")
+    before = [p.detach().clone() for p in m.parameters()]
+    with pytest.raises(FloatingPointError, match="not applied"):
+        train_step(m, opt, ids, targets, precision="fp32")
+    assert all(p.grad is None for p in m.parameters())
+    assert not opt.state
+    for p, b in zip(m.parameters(), before):
+        assert torch.equal(p.nan_to_num(), b.nan_to_num())
