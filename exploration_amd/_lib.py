@@ -38,6 +38,9 @@ SIGNATURES = {
                       + [_i64p, _f32p, _f32p, _i64, ctypes.c_int, _p, _f32p, _p, _sz, _p]),
     "st_sparse_fwd": (ctypes.c_int, [ctypes.c_int] + [_i64] * 6 + [_p, _i64p, _p, _p, _i32p] + [_i64] * 4
                       + [_p, _i64p, _f32p, _f32p, _f32p, _p, _sz, _p]),
+    "st_sparse_noalloc_scratch_bytes": (_sz, []),
+    "st_sparse_fwd_noalloc": (ctypes.c_int, [ctypes.c_int] + [_i64] * 6 + [_p, _i64p, _p, _p, _i32p]
+                              + [_i64] * 4 + [_p, _i64p, _f32p, _f32p, _f32p, _p]),
     "st_halo_supported": (ctypes.c_int, [ctypes.c_int, _i64, _i64]),
     "st_halo_attn_fwd": (ctypes.c_int, [ctypes.c_int] + [_i64] * 8 + [_p, _f32p, _f32p, _p, _p]),
     "st_halo_attn_bwd": (ctypes.c_int, [ctypes.c_int] + [_i64] * 8 + [_p, _f32p, _f32p, _p, _p, _p, _p]),

@@ -6,6 +6,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 
 #include "../../include/st_attn.h"
@@ -506,3 +507,74 @@ int st_halo_attn_bwd(int dtype, int64_t batch, int64_t groups, int64_t block_siz
   a.dqkv = dqkv;
   return launched(st::launch_halo_bwd(dtype, a, as_stream(stream)), "st_halo_attn_bwd");
 }
+
+// ---------------------------------------------------------------------------
+// sparse forward without a caller workspace
+
+namespace {
+
+// The workspace of st_sparse_fwd_noalloc: the block scores of every row
+// followed by the read's slot partials. One copy per GPU (the module's
+// device globals), held until the process ends; every call on a GPU reuses
+// and overwrites it. Host code never passes the array's name to a kernel: it
+// uses the device address looked up below.
+constexpr size_t kScratchBytes = ST_SPARSE_NOALLOC_SCRATCH_BYTES;
+__device__ __attribute__((aligned(256))) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device, null until looked up
+
+// Device address of the current device's `scratch`, looked up once per
+// device (hipGetSymbolAddress with that device current).
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return launched(e, "st_sparse_fwd_noalloc (hipGetDevice)");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(ST_EUNSUPPORTED, "st_sparse_fwd_noalloc: device %d beyond the %d supported", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return launched(e, "st_sparse_fwd_noalloc (hipGetSymbolAddress)");
+    if (!p) return fail(ST_ELAUNCH, "st_sparse_fwd_noalloc: no device address for the scratch array");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return ST_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t st_sparse_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+int st_sparse_fwd_noalloc(int dtype, int64_t batch, int64_t queries, int64_t heads, int64_t head_dim,
+                          int64_t block_size, int64_t topk, const void* q, const int64_t* positions,
+                          const void* k, const void* v, const int32_t* page_table, int64_t page_tokens,
+                          int64_t pages_per_seq, int64_t n_tokens, int64_t token_offset, void* out,
+                          int64_t* ids, float* top_scores, float* log_zr, float* lse, void* stream) {
+  int e;
+  if ((e = check_dtype(dtype)) || (e = check_sizes(batch, queries, 1, heads, head_dim, block_size)) ||
+      (e = check_envelope(head_dim, block_size)) ||
+      (e = check_kv("st_sparse_fwd_noalloc", block_size, k, page_table, page_tokens, pages_per_seq, n_tokens,
+                    token_offset)))
+    return e;
+  if (topk < 1) return fail(ST_EINVAL, "topk positive; cache pages/offset must be block aligned");
+  const int64_t n_blocks = (n_tokens + block_size - 1) / block_size;
+  const size_t need = st_sparse_workspace_bytes(batch, queries, heads, head_dim, topk, n_blocks);
+  if (need > kScratchBytes)
+    return fail(ST_EUNSUPPORTED,
+                "st_sparse_fwd_noalloc: this problem needs %zu bytes of scratch, the built-in array holds %zu "
+                "(call st_sparse_fwd with a workspace)",
+                need, kScratchBytes);
+  void* ws = nullptr;
+  if ((e = scratch_address(&ws))) return e;
+  return st_sparse_fwd(dtype, batch, queries, heads, head_dim, block_size, topk, q, positions, k, v, page_table,
+                       page_tokens, pages_per_seq, n_tokens, token_offset, out, ids, top_scores, log_zr, lse, ws,
+                       kScratchBytes, stream);
+}
+
+}  // extern "C"

@@ -160,6 +160,24 @@ int st_sparse_fwd(int dtype, int64_t batch, int64_t queries, int64_t heads, int6
                   int64_t* ids, float* top_scores, float* log_zr, float* lse, void* workspace,
                   size_t workspace_bytes, void* stream);
 
+/* st_sparse_fwd without a caller workspace. No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). The
+ * workspace is a file-scope device array of ST_SPARSE_NOALLOC_SCRATCH_BYTES
+ * per GPU, held until the process ends; problems whose workspace
+ * (st_sparse_workspace_bytes) exceeds it fail with ST_EUNSUPPORTED. Calls
+ * that overlap on one GPU (concurrent streams or threads) share that array
+ * and race: serialise them. Same arguments and results as st_sparse_fwd;
+ * allocates nothing (the first call on a device looks up the array's
+ * device address). */
+#define ST_SPARSE_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+size_t st_sparse_noalloc_scratch_bytes(void);
+int st_sparse_fwd_noalloc(int dtype, int64_t batch, int64_t queries, int64_t heads, int64_t head_dim,
+                          int64_t block_size, int64_t topk, const void* q, const int64_t* positions,
+                          const void* k, const void* v, const int32_t* page_table, int64_t page_tokens,
+                          int64_t pages_per_seq, int64_t n_tokens, int64_t token_offset, void* out,
+                          int64_t* ids, float* top_scores, float* log_zr, float* lse, void* stream);
+
 /* Two-block window attention of the model's local blocks (no st.ops
  * counterpart: the reference computes it with torch's scaled dot-product
  * attention, st/models/blocks.py:131-160, after the rotary embedding of

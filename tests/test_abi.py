@@ -92,6 +92,27 @@ def test_argument_errors_map_to_value_error():
     assert lib.st_dense_fwd_workspace_bytes(0, 1, 3, 3, 1, 17, 4) == 5 * pad(3 * 24 * 4)
 
 
+def test_noalloc_entry_point_rejects_problems_beyond_its_array():
+    """st_sparse_fwd_noalloc checks the workspace its problem needs against
+    its fixed array on the host, before any HIP call: the pointers below are
+    never dereferenced."""
+    lib = _lib.load()
+    assert lib.st_sparse_noalloc_scratch_bytes() == 16 << 20
+    batch, queries, heads, dim, b, topk, n = 1, 64, 32, 128, 16, 64, 1 << 20  # 256 MiB of block scores
+    need = lib.st_sparse_workspace_bytes(batch, queries, heads, dim, topk, n // b)
+    assert need > lib.st_sparse_noalloc_scratch_bytes()
+    fake = ctypes.c_void_p(256)
+    status = lib.st_sparse_fwd_noalloc(2, batch, queries, heads, dim, b, topk, fake, fake, fake, fake, None, b, 0,
+                                       n, 0, fake, fake, fake, fake, None, None)
+    assert status == _lib.ST_EUNSUPPORTED
+    assert b"built-in array holds" in lib.st_last_error()
+    with pytest.raises(ValueError, match="scratch"):
+        _lib.check(status, lib)
+    status = lib.st_sparse_fwd_noalloc(2, batch, queries, heads, dim, b, 0, fake, fake, fake, fake, None, b, 0,
+                                       n, 0, fake, fake, fake, fake, None, None)
+    assert status == _lib.ST_EINVAL and b"topk positive" in lib.st_last_error()
+
+
 def test_python_entry_points_validate_like_the_reference():
     from exploration_amd import TensorPages, dense_attention, sparse_attention
     q = torch.zeros(1, 2, 1, 8)
