@@ -1,12 +1,14 @@
-// Gated dense block attention, forward: pipelined gfx950 path for 16-bit
-// inputs with head_dim 64 or 128 (the hot shapes). Same algorithm as
-// dense_fwd.hip (remote pass with one exp per score and block sums, remote
-// mean parked in RC, then the local window pass); this variant
+// Gated dense block attention, forward: gfx950 path for 16-bit inputs with
+// head_dim 64 or 128 (the hot shapes). Same algorithm as dense_fwd.hip
+// (remote pass with one exp per score and block sums, remote mean parked in
+// RC, then the local window pass); this variant
+//  * runs two waves per SIMD in two phase-shifted groups (see the kernel),
+//    so that one wave's MFMAs overlap the other's softmax;
 //  * stages each 128-key K/V tile with asynchronous global->LDS copies into a
-//    swizzled row-major layout, double-buffered so the copies of tile i+1
-//    overlap the arithmetic of tile i;
+//    swizzled row-major layout, one group's copies during its softmax phase;
 //  * reads K fragments with ds_read_b128 and V^T fragments with
-//    ds_read_tr16_b64 (no transposed LDS stores);
+//    ds_read_tr16_b64 (no transposed LDS stores), Q fragments from LDS in
+//    register order;
 //  * fixes the block size at compile time;
 //  * numbers workgroups head-fastest so consecutive workgroups, which the
 //    dispatcher spreads over the XCDs, keep one head's K/V per XCD L2.
@@ -18,32 +20,52 @@
 
 namespace st {
 
-// Cost of splitting a row tile into two pieces, in key tiles (~2.8 us each
-// at D=128): the second workgroup's dispatch, prologue, first (cold) tiles
-// and epilogue, and the merge. Measured on cfg2 over 1..8 and "never": 6 is
-// the fastest (78 us against 88 at 3 and 98 never splitting).
-constexpr int kPieceCost = 6;
+// Cost of splitting a row tile into two pieces, in key tiles: the second
+// workgroup's dispatch, prologue (Q fragments, first K tile), epilogue (the
+// two groups' join) and the merge kernel's share. Measured on cfg2's
+// forward (with the merge) over 0..24 and "never": 12 is the fastest
+// (76.5 us against 81.2 at 6, 84.9 at 0 and 82.1 never splitting).
+constexpr int kPieceCost = 12;
 
+// A work item is 128 query rows of one (batch, head), run by eight waves in
+// two groups of four (one wave of each group per SIMD). Wave w owns rows
+// 32(w%4)..+31 (lane = row on v_mfma_f32_32x32x16, score tiles transposed,
+// S^T = K Q^T). Group 0 takes the first of the item's remote key tiles and
+// then every local tile, group 1 the other remote tiles (counts balanced
+// between the groups). Each
+// group alternates MFMA phases (S^T products of its next tile, PV products
+// of its previous one) with softmax phases, one workgroup barrier after
+// each, and group 1 runs one phase behind group 0, so on every SIMD one
+// wave's MFMAs overlap the other's softmax. A group stages its own K/V tiles
+// (one buffer each) during its softmax phase. At the end group 1's partial
+// remote state joins group 0's through LDS (the exact combination of two
+// online-softmax states that dense_fwd_merge also uses).
 template <typename T, int DP, int LOGB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void dense_fwd_fast_kernel(DenseArgs a, int n_qtiles) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void dense_fwd_fast_kernel(DenseArgs a, int n_qtiles) {
   typedef Mma<T> M;
   typedef typename M::Frag Frag;
-  constexpr int WAVES = 4;
+  constexpr int WAVES = 8;
   constexpr int NT = 128;
   constexpr int NST = NT / 32;
   constexpr int NDT = DP / 32;
   constexpr int NKC = DP / M::KW;
   constexpr int TILE = NT * DP;
-  // Two K and two V buffers as distinct LDS objects, selected at compile
-  // time, so the compiler can tell the copies into one buffer from the reads
-  // of the other and does not wait for the copies before reading.
-  __shared__ __attribute__((aligned(16))) T k0s[TILE];
-  __shared__ __attribute__((aligned(16))) T k1s[TILE];
-  __shared__ __attribute__((aligned(16))) T v0s[TILE];
-  __shared__ __attribute__((aligned(16))) T v1s[TILE];
-  __shared__ int range[2][4][WAVES];  // two tiles: this one and the pair partner
+  // The item's Q fragments (in register order: fragment c of lane l of the
+  // waves owning rows 32w..32w+31 at 512 (4 c + w) + 8 l elements), then K
+  // of group 0 and group 1, then V of group 0 and group 1: 160 KiB at head
+  // dim 128. One LDS object (the per-lane fragment offsets below carry the
+  // group's buffers, so every read is one address register plus an
+  // immediate); the copies into a group's buffers are waited for before that
+  // group's next reads anyway. The key-range table (before Q is stored) and
+  // the epilogue's per-row statistics (after the last Q read) use the Q area.
+  __shared__ __attribute__((aligned(16))) T kvs[5][TILE];
+  int (*range)[4][WAVES] = reinterpret_cast<int (*)[4][WAVES]>(&kvs[0][0]);  // [2][4][WAVES]
+  float (*xrow)[128] = reinterpret_cast<float (*)[128]>(&kvs[0][0]);         // [3][128]
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  // wave-uniform (scalar): the group branches stay scalar branches
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2, wg = wave & 3;
   const int col = lane & 31, half = lane >> 5;
   const int BH = a.B * a.H;
   const int bh = blockIdx.x % BH, slot = blockIdx.x / BH;
@@ -68,7 +90,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     int rlim, llo, lhi;
   };
   auto row_keys = [&](int qt) -> RowKeys {
-    const int row = qt * 32 * WAVES + wave * 32 + col;
+    const int row = qt * 128 + wg * 32 + col;
     RowKeys r = {row < a.Q ? a.pos[(int64_t)bi * a.Q + row] : -1, 0, 0, -1};
     if (r.p >= 0) {
       const int64_t c = r.p >> LOGB;
@@ -104,8 +126,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       rg2 = max(rg2, range[k][2][w]);
       rg3 = min(rg3, range[k][3][w]);
     }
-    // uniform by construction; in SGPRs, everything derived from them (tile
-    // indices, loop bounds, staging addresses) stays scalar
     rg0 = __builtin_amdgcn_readfirstlane(rg0);
     rg1 = __builtin_amdgcn_readfirstlane(rg1);
     rg2 = __builtin_amdgcn_readfirstlane(rg2);
@@ -166,42 +186,55 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
     if (kind == 1 && !split) return;  // whole workgroup
   }
-  const int row = qt * 32 * WAVES + wave * 32 + col;
+  const int row = qt * 128 + wg * 32 + col;
   const bool row_in = row < a.Q;
   const RowKeys rk = row_keys(qt);
   const int64_t p = rk.p;
   const int rlim = rk.rlim, llo = rk.llo, lhi = rk.lhi;
-  const int full_remote = tk.full_remote, n_remote_all = tk.n_remote_all, lt0 = tk.lt0, n_local = tk.n_local;
+  // (all of the tile bookkeeping below is workgroup-uniform: kept in SGPRs
+  // so that the loop's branches are scalar)
+  const int full_remote = __builtin_amdgcn_readfirstlane(tk.full_remote);
+  const int n_remote_all = __builtin_amdgcn_readfirstlane(tk.n_remote_all);
+  const int lt0 = __builtin_amdgcn_readfirstlane(tk.lt0), n_local = __builtin_amdgcn_readfirstlane(tk.n_local);
   // A split row tile runs as two pieces: piece 0 takes remote tiles [0, h),
   // piece 1 remote tiles [h, n_remote_all) and the local tiles;
   // dense_fwd_merge combines their partial results.
   if (!split) hsplit = n_remote_all;
   const int piece = kind == 1;
   const int item = bh * n_qtiles + qt;
-  const int rs = piece ? hsplit : 0;                              // first remote tile of this piece
-  const int n_remote = piece ? n_remote_all - hsplit : hsplit;    // remote tiles of this piece
-  const bool with_local = !split || piece;
-  const int total = n_remote + (with_local ? n_local : 0);
-  auto tile_of = [&](int i) { return i < n_remote ? rs + i : lt0 + (i - n_remote); };
+  const int rs = __builtin_amdgcn_readfirstlane(piece ? hsplit : 0);               // first remote tile of this piece
+  const int n_remote = __builtin_amdgcn_readfirstlane(piece ? n_remote_all - hsplit : hsplit);  // remote tiles of this piece
+  const int n_loc = (!split || piece) ? n_local : 0;  // local tiles of this piece
+  // this group's tiles: group 0 the first r0 remote tiles, then the local
+  // ones; group 1 the other remote tiles (r0 balances the two counts)
+  const int r0 = __builtin_amdgcn_readfirstlane(min(n_remote, max(0, (n_remote - n_loc + 1) / 2)));
+  const int my_remote = grp ? n_remote - r0 : r0;
+  const int my_first = grp ? rs + r0 : rs;  // first remote tile of this group
+  const int my_n = my_remote + (grp ? 0 : n_loc);
+  auto tile_of = [&](int k) __attribute__((always_inline)) {
+    return k < my_remote ? my_first + k : lt0 + (k - my_remote);
+  };
 
   const T* kg = reinterpret_cast<const T*>(a.k) + ((int64_t)bi * N * H + hh) * D;
   const T* vg = reinterpret_cast<const T*>(a.v) + ((int64_t)bi * N * H + hh) * D;
   const int64_t kstride = H * D;
-  const Stager<T, DP, WAVES> kst(kg, kstride, a.N), vst(vg, kstride, a.N);
-
-  Frag qf[NKC];
-  {
-    const T* qrow = reinterpret_cast<const T*>(a.q) + (((int64_t)bi * a.Q + (row_in ? row : 0)) * H + hh) * D;
-#pragma unroll
-    for (int c = 0; c < NKC; ++c) qf[c] = row_in ? *reinterpret_cast<const Frag*>(qrow + c * 16 + half * 8) : Frag{};
-  }
+  // each group stages its own tiles
+  const int gtid = (int)threadIdx.x & 255;
+  const Stager<T, DP, 4> kst(kg, kstride, a.N, gtid), vst(vg, kstride, a.N, gtid);
+  T* const lds = &kvs[0][0];
+  T* const kbuf = lds + (1 + grp) * TILE;
+  T* const vbuf = lds + (3 + grp) * TILE;
+  // this lane's Q fragments: element offset of fragment c is qoff + 2048 c
+  // (NKC fragments of 4 waves x 64 lanes x 8 elements fill the Q area)
+  static_assert(NKC * 2048 == TILE, "Q fragments fill one tile");
+  const int qoff = 512 * wg + 8 * lane;
 
   // Per-lane LDS fragment offsets (elements). The swizzle of a fragment row
   // depends only on the lane (tile row offsets are multiples of 16), so the
-  // subtile and buffer parts of every address are compile-time immediates.
+  // subtile parts of every address are compile-time immediates.
   int koff[NKC];
 #pragma unroll
-  for (int c = 0; c < NKC; ++c) koff[c] = col * DP + (((2 * c + half) ^ swz<DP>(col)) * 8);
+  for (int c = 0; c < NKC; ++c) koff[c] = (1 + grp) * TILE + col * DP + (((2 * c + half) ^ swz<DP>(col)) * 8);
   int voff[NDT], voff8[NDT];  // rows r0 and r0 + 8 (swizzled separately)
   {
     const int gi = lane >> 4, sl = lane & 15;
@@ -209,380 +242,388 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
       const int d = 32 * dt + 16 * (gi & 1) + 4 * (sl & 3);
-      voff[dt] = r0 * DP + (((d >> 3) ^ swz<DP>(r0)) * 8) + (d & 7);
-      voff8[dt] = (r0 + 8) * DP + (((d >> 3) ^ swz<DP>(r0 + 8)) * 8) + (d & 7);
+      voff[dt] = (3 + grp) * TILE + r0 * DP + (((d >> 3) ^ swz<DP>(r0)) * 8) + (d & 7);
+      voff8[dt] = (3 + grp) * TILE + (r0 + 8) * DP + (((d >> 3) ^ swz<DP>(r0 + 8)) * 8) + (d & 7);
     }
   }
   typedef short s4 __attribute__((ext_vector_type(4)));
   typedef short s8 __attribute__((ext_vector_type(8)));
-  auto kfrag = [&](const T* buf, int st, int c) -> Frag {
-    return *reinterpret_cast<const Frag*>(buf + 32 * st * DP + koff[c]);
+  // (fragments of this group's K and V tiles)
+  auto kfrag = [&](int st, int c) __attribute__((always_inline)) -> Frag {
+    return *reinterpret_cast<const Frag*>(lds + 32 * st * DP + koff[c]);
   };
-  auto vfrag = [&](const T* buf, int k0, int dt) -> Frag {
-    const T* p0 = buf + k0 * DP + voff[dt];
-    const T* p1 = buf + k0 * DP + voff8[dt];
+  auto vfrag = [&](int k0, int dt) __attribute__((always_inline)) -> Frag {
+    const T* p0 = lds + k0 * DP + voff[dt];
+    const T* p1 = lds + k0 * DP + voff8[dt];
     s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)p0);
     s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)p1);
     return __builtin_bit_cast(Frag, (s8)__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   };
 
-  // PV accumulator (acc^T[d][row], lane = row): the remote pass, then the
-  // local pass
+  // PV accumulator (acc^T[d][row], lane = row): the remote pass, then (group
+  // 0) the local pass
   f32x16 acc[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) acc[dt] = zero16();
   const int64_t obase = (((int64_t)bi * a.Q + row) * H + hh) * D;
   // running state of the remote pass (max, row sum, sum of squared block
-  // sums) and of the local pass (max, row sum); maxima in log2 units
+  // sums) and of the local pass (max, row sum); maxima in log2 units; the
+  // sums are this lane's part (its half of the row's keys), joined with the
+  // other half when the pass ends
   float m_r = kNegInf, zs_r = 0.f, dr = 0.f, m_l = kNegInf, zs_l = 0.f;
-  float log_zr = kNegInf, lr = kNegInf;
 
-  // End of the remote pass: its statistics, and its mean parked in rc (one
-  // burst of stores that drains while the local tiles run; registers cannot
-  // hold two accumulators next to the pipelined loop).
-  const bool park_rc = !(split && piece == 0);  // piece 0 writes its mean in the epilogue
-  auto finish_remote = [&]() {
+  // Group 0's end of the remote pass: join the halves of its sums and, when
+  // local tiles follow, park its remote mean acc/dr in rc (one burst of
+  // stores that drains while the local tiles run).
+  const bool park_rc = !(split && piece == 0);  // piece 0 keeps its remote sums for the epilogue
+  auto finish_remote = [&]() __attribute__((always_inline)) {
     zs_r += swap_halves(zs_r);
     dr += swap_halves(dr);
-    log_zr = log_mass(m_r, zs_r);
-    lr = dr > 0.f ? log_mass(m_r, dr) - fast_log2(zs_r) * kLn2 : kNegInf;
-    const float inv = dr > 0.f ? 1.f / dr : 0.f;
-    if (row_in && park_rc) {
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int d = 32 * dt + 8 * i + 4 * half;
-          f32x4 val = {acc[dt][4 * i] * inv, acc[dt][4 * i + 1] * inv, acc[dt][4 * i + 2] * inv,
-                       acc[dt][4 * i + 3] * inv};
-          *reinterpret_cast<f32x4*>(a.rc + obase + d) = val;
-        }
-    }
-    // the local pass starts from zero; piece 0 keeps its remote sums for
-    // the epilogue
     if (park_rc) {
+      const float inv = dr > 0.f ? 1.f / dr : 0.f;
+      if (row_in) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int d = 32 * dt + 8 * i + 4 * half;
+            f32x4 val = {acc[dt][4 * i] * inv, acc[dt][4 * i + 1] * inv, acc[dt][4 * i + 2] * inv,
+                         acc[dt][4 * i + 3] * inv};
+            *reinterpret_cast<f32x4*>(a.rc + obase + d) = val;
+          }
+      }
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) acc[dt] = zero16();
     }
   };
 
-  // Software pipeline over the tile sequence. Iteration i issues, in one
-  // scheduling region, the PV MFMAs of tile i-1 (V buffer (i+1)&1) while the
-  // VALU masks, maximises and exponentiates the scores of tile i, then the
-  // S^T MFMAs of tile i+1 (K buffer (i+1)&1) while the VALU scales and
-  // converts tile i to 16-bit probabilities; the S^T products of subtile st
-  // overwrite scores the softmax has finished with, so one score buffer and
-  // one probability buffer suffice. Products go in chunks of 4 with their LDS
-  // reads one chunk ahead. Past the ends of the sequence the MFMAs run on
-  // finite filler data whose results are never used (probabilities of tile
-  // -1 are zero; scores of tile `total` are discarded).
+  // scores of the group's current tile (S^T: keys x rows); after its
+  // softmax phase, the probabilities, converted to 16-bit PV operands in the
+  // next MFMA phase (where the vector unit is otherwise idle) before the next
+  // S^T products overwrite them
   f32x16 sc[NST];
-  Frag pf[NST][2];
 #pragma unroll
-  for (int st = 0; st < NST; ++st)
+  for (int st = 0; st < NST; ++st) sc[st] = zero16();
+  // per subtile: the factor the probabilities are multiplied by when they
+  // become PV operands (remote blocks of 32+ keys: the block sum, applied
+  // in the MFMA phase, whose vector unit is otherwise idle; else 1)
+  float gate[NST];
 #pragma unroll
-    for (int c2 = 0; c2 < 2; ++c2) pf[st][c2] = Frag{};
-  constexpr int NSP = NST * NKC;      // S^T products per tile
-  constexpr int NPV = NST * 2 * NDT;  // PV products per tile
-  constexpr int H1 = NPV / 4;         // chunks of the first half (PV)
-  constexpr int H2 = NSP / 4;         // chunks of the second half (S^T)
-  constexpr int CPS = H2 / NST;       // chunks per score subtile
-  static_assert(NPV % 4 == 0 && NSP % 4 == 0 && H2 % NST == 0, "chunks of 4 products");
-  constexpr int NSL1 = 10;            // first-half softmax slices
+  for (int st = 0; st < NST; ++st) gate[st] = 1.f;
 
-  float mt = kNegInf, msafe = 0.f, alpha = 1.f, psum = 0.f, blk1 = 0.f;
-  bool grow = false;
-  float blkv[NST][8];
-  // First-half slice K: masks and row max (K < 2), exponentials (K >= 2).
-  auto slice1 = [&]<int K, bool MASKED>(bool remote, int kb) {
-    if constexpr (K < 2) {
-      constexpr int s0 = K * ((NST + 1) / 2);
-      constexpr int s1 = K ? NST : (NST + 1) / 2;
-      if constexpr (MASKED) {
-        // key of register r in subtile st is kb + 4*half + (32*st + 8*(r/4) + r%4)
-        const int base = kb + 4 * half;
-        const int lim = (remote ? rlim : lhi + 1) - base;
-        const int lo = remote ? INT32_MIN : llo - base;
+  // MFMA phase k: PV products of the group's tile k-1 (V in vbuf) first,
+  // then the S^T products of its tile k (K in kbuf), in chunks of 4 with the
+  // LDS reads of the next chunk issued one chunk ahead.
+  constexpr int NPV = NST * 2 * NDT;  // PV products per tile (16 keys x 32 dims each)
+  constexpr int NSP = NST * NKC;      // S^T products per tile
+  // Phase 0 multiplies the zero probabilities by the zeroed V buffer, and
+  // phase n's S^T products (of the group's last K tile again) are discarded:
+  // one code path for every phase.
+  auto mfma_phase = [&](int k) __attribute__((always_inline)) {
+    auto pv_load = [&](int q) __attribute__((always_inline)) { return vfrag(16 * (q / NDT), q % NDT); };
+    auto pv_mma = [&](int q, Frag f) __attribute__((always_inline)) {
+      const int st = q / (2 * NDT), c2 = (q / NDT) & 1;
+      Frag b;
 #pragma unroll
-        for (int st = s0; st < s1; ++st)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int off = 32 * st + 8 * (r >> 2) + (r & 3);
-            sc[st][r] = ((off < lim) & (off >= lo)) ? sc[st][r] : kNegInf;
-          }
-      }
-#pragma unroll
-      for (int st = s0; st < s1; ++st)
-#pragma unroll
-        for (int r = 0; r < 16; r += 2) mt = fmaxf(mt, fmaxf(sc[st][r], sc[st][r + 1]));
-      if constexpr (K == 1) {
-        mt = fmaxf(mt, swap_halves(mt)) * a.scale_log2;
-        // lazy rescaling: the max only moves when some row of the wave
-        // exceeds it by more than kLazyLog2 (alpha is exactly 1 otherwise)
-        const float m = remote ? m_r : m_l;
-        grow = __builtin_amdgcn_ballot_w64(mt > m + kLazyLog2) != 0;
-        const float mn = grow ? fmaxf(m, mt) : m;
-        msafe = mn == kNegInf ? 0.f : mn;
-        alpha = fast_exp2(m - msafe);
-        if (remote) m_r = mn;
-        else m_l = mn;
-        mt = kNegInf;
-        psum = 0.f;
-      }
-    } else {
-      constexpr int v0 = (16 * NST) * (K - 2) / 8, v1 = (16 * NST) * (K - 1) / 8;
-#pragma unroll
-      for (int v = v0; v < v1; ++v) {
-        const float x = fast_exp2(fmaf(sc[v / 16][v % 16], a.scale_log2, -msafe));
-        sc[v / 16][v % 16] = x;
-        psum += x;
-      }
-    }
+      for (int e = 0; e < 8; ++e) b[e] = from_float<T>(sc[st][8 * c2 + e] * gate[st]);
+      acc[q % NDT] = M::mma(f, b, acc[q % NDT]);
+    };
+    // S^T products contraction chunk outermost (product j: chunk j / NST,
+    // subtile j % NST), so each Q fragment is read once per phase
+    auto s_load = [&](int j) __attribute__((always_inline)) { return kfrag(j % NST, j / NST); };
+    Frag qc;
+    auto s_mma = [&](int j, Frag f) __attribute__((always_inline)) {
+      const int st = j % NST, c = j / NST;
+      if (st == 0) qc = *reinterpret_cast<const Frag*>(lds + qoff + 2048 * c);
+      sc[st] = M::mma(f, qc, c == 0 ? zero16() : sc[st]);
+    };
+    mfma_chunks<NPV + NSP, 4, NPV>(
+        [&](int j) __attribute__((always_inline)) { return j < NPV ? pv_load(j) : s_load(j - NPV); },
+        [&](int j, Frag f) __attribute__((always_inline)) {
+          if (j < NPV) pv_mma(j, f);
+          else s_mma(j - NPV, f);
+        });
+    // group 0: the last remote PV products (tile my_remote - 1) are in
+    if (grp == 0 && k == my_remote) finish_remote();
   };
-  // Second-half slice for score subtile ST: the block scaling (remote pass)
-  // and the conversion to 16-bit probabilities, after which sc[ST] is free.
-  auto slice2 = [&]<int ST>(bool remote) {
-    if constexpr (ST == 0) {
-      if (remote) zs_r = zs_r * alpha + psum;
-      else zs_l = zs_l * alpha + psum;
-      if (remote) {
-        if constexpr ((1 << LOGB) == NT) {
-          // the tile is one block: its row sum is the block sum
-          blk1 = psum + swap_halves(psum);
-          dr = dr * (alpha * alpha) + psum * blk1;
-        } else {
-          block_sums<NST, LOGB>(sc, blkv);
-          dr *= alpha * alpha;
-        }
-      }
-    }
-    if (remote) {
-      if constexpr ((1 << LOGB) == NT) {
-        sc[ST] *= blk1;
-      } else {
-        float w = 0.f;
+
+  // Softmax phase of the group's tile k: masks, the row max (lazy
+  // rescaling: the max only moves when some row of the wave exceeds it by
+  // more than kLazyLog2), exponentials, the row and block sums, the gate
+  // (remote tiles: each probability times its block's sum), the 16-bit
+  // probabilities for PV, and the accumulator's rescale before the PV
+  // products of tile k.
+  auto softmax_phase = [&]<bool MASKED>(int k) __attribute__((always_inline)) {
+    const bool remote = k < my_remote;
+    const int kb = tile_of(k) * NT;
+    if constexpr (MASKED) {
+      // key of register r in subtile st: kb + 4*half + 32*st + 8*(r/4) + r%4;
+      // visible iff lo <= offset < lim (one unsigned compare)
+      const int base = kb + 4 * half;
+      const int lim = (remote ? rlim : lhi + 1) - base;
+      const int lo = remote ? -(1 << 30) : llo - base;
+      const uint32_t span = lim > lo ? (uint32_t)(lim - lo) : 0u;
+#pragma unroll
+      for (int st = 0; st < NST; ++st)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          sc[ST][r] *= blkv[ST][blk_slot<LOGB>(r)];
-          w += sc[ST][r];
+          const int off = 32 * st + 8 * (r >> 2) + (r & 3);
+          sc[st][r] = (uint32_t)(off - lo) < span ? sc[st][r] : kNegInf;
         }
-        dr += w;
+    }
+    // balanced trees (short dependency chains)
+    float mx4[NST];
+#pragma unroll
+    for (int st = 0; st < NST; ++st) mx4[st] = tree16<OpMax>(sc[st]);
+    float mt = fmaxf(fmaxf(mx4[0], mx4[1]), fmaxf(mx4[2], mx4[3]));
+    mt = fmaxf(mt, swap_halves(mt)) * a.scale_log2;
+    const float m = remote ? m_r : m_l;
+    const bool grow = __builtin_amdgcn_ballot_w64(mt > m + kLazyLog2) != 0;
+    const float mn = grow ? fmaxf(m, mt) : m;
+    const float msafe = mn == kNegInf ? 0.f : mn;
+    const float alpha = fast_exp2(m - msafe);
+    if (remote) m_r = mn;
+    else m_l = mn;
+#pragma unroll
+    for (int st = 0; st < NST; ++st)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sc[st][r] = fast_exp2(fmaf(sc[st][r], a.scale_log2, -msafe));
+    // in-lane sums per subtile, and the lane's part of the row sum
+    float ps[NST];
+#pragma unroll
+    for (int st = 0; st < NST; ++st) ps[st] = tree16<OpAdd>(sc[st]);
+    const float psum = (ps[0] + ps[1]) + (ps[2] + ps[3]);
+    if (remote) {
+      zs_r = zs_r * alpha + psum;
+      if constexpr (LOGB >= 5) {
+        // blocks of whole subtiles: block totals from the subtile sums
+        constexpr int G = (1 << LOGB) / 32;
+        float blk[NST];
+        float w = 0.f;
+#pragma unroll
+        for (int g0 = 0; g0 < NST; g0 += G) {
+          float part = ps[g0];
+#pragma unroll
+          for (int g = 1; g < G; ++g) part += ps[g0 + g];
+          const float tot = part + swap_halves(part);
+          w += part * tot;  // this lane's keys of the block times the block sum
+#pragma unroll
+          for (int g = 0; g < G; ++g) blk[g0 + g] = tot;
+        }
+        dr = dr * (alpha * alpha) + w;
+#pragma unroll
+        for (int st = 0; st < NST; ++st) gate[st] = blk[st];  // applied in the MFMA phase
+      } else {
+        float blkv[NST][8];
+        block_sums<NST, LOGB>(sc, blkv);
+        float w = 0.f;
+#pragma unroll
+        for (int st = 0; st < NST; ++st)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            sc[st][r] *= blkv[st][blk_slot<LOGB>(r)];
+            w += sc[st][r];
+          }
+        dr = dr * (alpha * alpha) + w;
+      }
+    } else {
+      zs_l = zs_l * alpha + psum;
+    }
+    if constexpr (LOGB >= 5) {
+      if (!remote) {
+#pragma unroll
+        for (int st = 0; st < NST; ++st) gate[st] = 1.f;
       }
     }
-#pragma unroll
-    for (int c2 = 0; c2 < 2; ++c2) pf[ST][c2] = frag_from_c<T>(sc[ST], c2);
-  };
-
-  // MASKED = false: an unmasked remote tile (the bulk); MASKED = true: any
-  // tile, remote or local, with the causal / window masks applied.
-  auto iteration = [&]<int PAR, bool MASKED>(int i) {
-    const bool remote = MASKED ? i < n_remote : true;
-    wait_vm();
-    __syncthreads();
-    if (i + 2 < total) kst.template stage<NT>(PAR ? k1s : k0s, tile_of(i + 2) * NT);
-    vst.template stage<NT>(PAR ? v1s : v0s, tile_of(i) * NT);
-    const T* kt = PAR ? k0s : k1s;
-    const T* vt = PAR ? v0s : v1s;
-    const int kb = tile_of(i) * NT;
-    // chunk g < H1: PV products 4g..4g+3 (head-dim tile q % NDT, 16-key chunk
-    // q / NDT); chunk H1 + h: S^T subtile h / CPS, contraction chunks
-    // 4 (h % CPS) .. +3
-    auto load = [&](int g, int u) -> Frag {
-      if (g < H1) {
-        const int q = 4 * g + u;
-        return vfrag(vt, 16 * (q / NDT), q % NDT);
-      }
-      const int h = g - H1;
-      return kfrag(kt, h / CPS, 4 * (h % CPS) + u);
-    };
-    Frag buf[2][4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) buf[0][u] = load(0, u);
-    [&]<int... G>(std::integer_sequence<int, G...>) {
-      ([&] {
-        constexpr int g = G;
-        __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this chunk's reads
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (g + 1 < H1 + H2) {
-#pragma unroll
-          for (int u = 0; u < 4; ++u) buf[(g + 1) & 1][u] = load(g + 1, u);
-        }
-        if constexpr (g < H1) {
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int q = 4 * g + u;
-            acc[q % NDT] = M::mma(buf[g & 1][u], pf[q / (2 * NDT)][(q / NDT) & 1], acc[q % NDT]);
-          }
-          [&]<int... L>(std::integer_sequence<int, L...>) {
-            (slice1.template operator()<g * NSL1 / H1 + L, MASKED>(remote, kb), ...);
-          }(std::make_integer_sequence<int, (g + 1) * NSL1 / H1 - g * NSL1 / H1>{});
-        } else {
-          constexpr int h = g - H1, st = h / CPS;
-          if constexpr (h % CPS == 0) slice2.template operator()<st>(remote);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int c = 4 * (h % CPS) + u;
-            sc[st] = M::mma(buf[g & 1][u], qf[c], c == 0 ? zero16() : sc[st]);
-          }
-        }
-      }(), ...);
-    }(std::make_integer_sequence<int, H1 + H2>{});
-    __builtin_amdgcn_sched_barrier(0);
-    // the last remote PV products (tile i-1) are in: park the remote pass;
-    // otherwise a raised max rescales the accumulator before the PV products
-    // of tile i (next iteration)
-    if (i == n_remote) {
-      finish_remote();
-    } else if (grow) {
+    if (grow) {
+      // acc holds the sums of earlier tiles at the old max (squared for the
+      // remote pass, whose weights carry two factors of 2^-m)
       const float f = remote ? alpha * alpha : alpha;
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) acc[dt] *= f;
     }
   };
 
-  if (total > 0) {
-    // prologue: K of tiles 0 and 1, finite filler in the V buffer iteration 0
-    // reads, then the S^T products of tile 0
-    kst.template stage<NT>(k0s, tile_of(0) * NT);
-    vst.template stage<NT>(v1s, tile_of(0) * NT);
-    if (total > 1) kst.template stage<NT>(k1s, tile_of(1) * NT);
-    wait_vm();
-    __syncthreads();
+  // Phases: MFMA(0), softmax(0), MFMA(1), ..., softmax(n-1), MFMA(n) for the
+  // group's n tiles, a barrier after each; group 1 starts one barrier later,
+  // and both groups end on the same barrier count. During softmax(k) the
+  // group stages K of its tile k+1 and V of its tile k (MFMA(k) has read the
+  // previous contents) and waits for the copies before the barrier.
+  const int my_bars = grp ? 2 * my_n + 2 : 2 * my_n + 1;
+  const int n0 = r0 + n_loc, n1 = n_remote - r0;
+  const int all_bars = __builtin_amdgcn_readfirstlane(max(2 * n0 + 1, 2 * n1 + 2));
+  __syncthreads();  // the key-range table in the Q area is read
+  if (grp == 0) {
+    // Q fragments of this wave's rows (the B operands of S^T = K Q^T)
+    const T* qrow = reinterpret_cast<const T*>(a.q) + (((int64_t)bi * a.Q + (row_in ? row : 0)) * H + hh) * D;
 #pragma unroll
-    for (int st = 0; st < NST; ++st) sc[st] = zero16();
-    mfma_phase<NST * NKC, 4, 1>([&](int j) { return kfrag(k0s, j / NKC, j % NKC); },
-                                [&](int j, Frag f) { sc[j / NKC] = M::mma(f, qf[j % NKC], sc[j / NKC]); });
+    for (int c = 0; c < NKC; ++c)
+      *reinterpret_cast<Frag*>(lds + qoff + 2048 * c) =
+          row_in ? *reinterpret_cast<const Frag*>(qrow + c * 16 + half * 8) : Frag{};
   }
-  // unmasked remote tiles in pairs (an even count; an odd last one joins the
-  // masked loop), then every remaining tile through the masked variant
-  const int n_fast = max(0, min(full_remote, rs + n_remote) - rs) & ~1;
-  int i = 0;
-  for (; i < n_fast; i += 2) {
-    iteration.template operator()<0, false>(i);
-    iteration.template operator()<1, false>(i + 1);
+  if (my_n > 0) kst.template stage<NT>(kbuf, tile_of(0) * NT);
+  {
+    // zero V buffer for phase 0's PV products (16 bytes per thread and pass)
+    typedef typename Vec16<T>::type V;
+    V* z = reinterpret_cast<V*>(vbuf);
+#pragma unroll
+    for (int i = gtid; i < TILE / Vec16<T>::n; i += 256) z[i] = V{};
   }
-  for (; i < total; i += 2) {
-    iteration.template operator()<0, true>(i);
-    if (i + 1 < total) iteration.template operator()<1, true>(i + 1);
-  }
-  if (total > 0) {
-    // drain: PV products of the last tile
-    wait_vm();
+  wait_vm();
+  __syncthreads();
+  if (grp == 1) __syncthreads();
+  auto step = [&]<bool MASKED>(int k) __attribute__((always_inline)) {
+    mfma_phase(k);
     __syncthreads();
-    const T* vt = (total - 1) & 1 ? v1s : v0s;
-    mfma_phase<NST * 2 * NDT, 4, 2>(
-        [&](int j) { return vfrag(vt, 16 * (j / NDT), j % NDT); },
-        [&](int j, Frag f) { acc[j % NDT] = M::mma(f, pf[j / (2 * NDT)][(j / NDT) & 1], acc[j % NDT]); });
-  }
-  if (total == n_remote) finish_remote();
-  // local statistics (zs now holds the local denominator); padding rows,
-  // which skipped masks on full remote tiles, have no mass at all
-  const float zsum = zs_l + swap_halves(zs_l);
-  constexpr int RLD = DP + 4;  // fp32 staging stride: conflict-free 16-byte writes
-  static_assert(32 * RLD * 4 + 32 * 4 <= TILE * (int)sizeof(T), "staging fits one buffer");
-  float* lst = reinterpret_cast<float*>(wave == 0 ? k0s : (wave == 1 ? k1s : (wave == 2 ? v0s : v1s)));
-  // acc * f (per row) into this wave's staging buffer, rows [32 wave, +32)
-  auto stage_acc = [&](float f) {
+    if (k < my_n) {
+      if (k + 1 < my_n) kst.template stage<NT>(kbuf, tile_of(k + 1) * NT);
+      vst.template stage<NT>(vbuf, tile_of(k) * NT);
+      softmax_phase.template operator()<MASKED>(k);
+      wait_vm();
+      __syncthreads();
+    }
+  };
+  // the group's unmasked tiles (remote tiles below every row's remote
+  // limit) come first: one loop per softmax variant
+  const int n_fast = __builtin_amdgcn_readfirstlane(min(my_remote, max(0, full_remote - my_first)));
+  int k = 0;
+  for (; k < n_fast; ++k) step.template operator()<false>(k);
+  for (; k <= my_n; ++k) step.template operator()<true>(k);
+  for (int i = my_bars; i < all_bars; ++i) __syncthreads();
+
+  // Epilogue. Every wave has passed the last barrier: the K/V buffers are
+  // free. Group 1 stages its remote mean (acc/dr, lane = row) and its
+  // statistics; group 0 joins them with its own state and writes the item's
+  // results (or the piece's partials for dense_fwd_merge) row-contiguously.
+  constexpr int CM = DP / 4 - 1;  // 16-byte chunks of a staged fp32 row, swizzled by the row
+  auto sidx = [](int r, int d) __attribute__((always_inline)) { return r * DP + ((((d >> 2) ^ (r & CM)) << 2) | (d & 3)); };
+  static_assert(2 * 32 * DP * 4 <= TILE * (int)sizeof(T), "two waves' rows fit one buffer");
+  float* stage1 = reinterpret_cast<float*>(kvs[1 + (wg >> 1)]) + (wg & 1) * 32 * DP;  // group 1's rows of wave wg
+  float* stage0 = reinterpret_cast<float*>(kvs[3 + (wg >> 1)]) + (wg & 1) * 32 * DP;  // group 0's rows of wave wg
+  auto stage_acc = [&](float* dst, float f) __attribute__((always_inline)) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int d = 32 * dt + 8 * i + 4 * half;
-        const f32x4 lv = {acc[dt][4 * i] * f, acc[dt][4 * i + 1] * f, acc[dt][4 * i + 2] * f,
-                          acc[dt][4 * i + 3] * f};
-        *reinterpret_cast<f32x4*>(lst + col * RLD + d) = lv;
+        const f32x4 v = {acc[dt][4 * i] * f, acc[dt][4 * i + 1] * f, acc[dt][4 * i + 2] * f, acc[dt][4 * i + 3] * f};
+        *reinterpret_cast<f32x4*>(dst + sidx(col, d)) = v;
       }
   };
-  if (a.fw0 != nullptr && !piece && threadIdx.x == 0) a.fflag[item] = split ? 1 : 0;
-  if (split) {
-    // partial results of this piece: statistics per row, and the remote mean
-    // (piece 0) or the local mean (piece 1) as rows, for dense_fwd_merge
-    const int lrow = wave * 32 + col;
-    float* st8 = a.fstat + ((size_t)item * 128 + lrow) * 8;
-    if (half == 0 && row_in) {
-      if (piece == 0) {
-        st8[0] = m_r; st8[1] = zs_r; st8[2] = dr;
-      } else {
-        st8[3] = m_r; st8[4] = zs_r; st8[5] = dr; st8[6] = m_l; st8[7] = zsum;
-      }
+  const int lrow = wg * 32 + col;  // row within the item
+  if (grp == 1) {
+    zs_r += swap_halves(zs_r);
+    dr += swap_halves(dr);
+    stage_acc(stage1, dr > 0.f ? 1.f / dr : 0.f);
+    if (half == 0) {
+      xrow[0][lrow] = m_r;
+      xrow[1][lrow] = zs_r;
+      xrow[2][lrow] = dr;
     }
-    const float f = piece == 0 ? (dr > 0.f ? 1.f / dr : 0.f) : (zsum > 0.f ? 1.f / zsum : 0.f);
-    float* dst = (piece == 0 ? a.fw0 : a.fw1) + (size_t)item * 128 * D;
-    __syncthreads();  // every wave is done with the K/V buffers
-    stage_acc(f);
-    __syncthreads();
-    constexpr int RL = DP / 4;  // lanes per row, 4 floats each
-    const int row0 = qt * 32 * WAVES + wave * 32;
-#pragma unroll
-    for (int it = 0; it < 32 * RL / 64; ++it) {
-      const int r = (it * 64 + lane) / RL, c = ((it * 64 + lane) % RL) * 4;
-      if (row0 + r < a.Q)
-        *reinterpret_cast<f32x4*>(dst + (int64_t)(wave * 32 + r) * D + c) =
-            *reinterpret_cast<const f32x4*>(lst + r * RLD + c);
-    }
-    return;
   }
-  const float dl = p >= 0 ? zsum : 0.f;
-  const float ll = p >= 0 ? log_mass(m_l, dl) : kNegInf;
-  if (p < 0) {
-    lr = kNegInf;
-    log_zr = kNegInf;
-  }
-  const float tot = logaddexp(lr, ll);
-  const float safe_total = tot == kNegInf ? 0.f : tot;
-  const float prem = lr == kNegInf ? 0.f : __expf(lr - safe_total);
-  const float ploc = ll == kNegInf ? 0.f : __expf(ll - safe_total);
-  const float linv = dl > 0.f ? ploc / dl : 0.f;
-  if (half == 0 && row_in) {
-    const int64_t sidx = ((int64_t)bi * a.Q + row) * H + hh;
-    a.pr[sidx] = prem;
-    a.zr[sidx] = log_zr;
-    a.z[sidx] = tot;
-  }
-  // rc = prem * (parked remote mean) and out = rc + ploc * (local mean), in
-  // row-contiguous form: each wave stages its 32 rows' local part and weights
-  // in one 32 KiB K/V buffer (free after the drain) and then reads, combines
-  // and writes whole rows. With lane = row, direct global accesses would
-  // touch 64 cache lines per instruction.
-  __syncthreads();  // every wave is done with the K/V buffers
-  float* wst = lst + 32 * RLD;  // per-row prem
-  stage_acc(linv);
-  if (half == 0) wst[col] = prem;
-  // the parked rc stores of this wave are visible to all its lanes
-  __threadfence_block();
   __syncthreads();
-  {
-    constexpr int RL = DP / 4;  // lanes per row, 4 floats each
-    const int row0 = qt * 32 * WAVES + wave * 32;
-    typedef T T4 __attribute__((ext_vector_type(4)));
-    constexpr int NIT = 32 * RL / 64;
-    // every load before the first store (the stores may alias in the
-    // compiler's view, which would serialise the round trips)
-    f32x4 mean[NIT];
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      const int r = (it * 64 + lane) / RL, c = ((it * 64 + lane) % RL) * 4;
-      const int64_t g = (((int64_t)bi * a.Q + row0 + r) * H + hh) * D + c;
-      mean[it] = row0 + r < a.Q ? *reinterpret_cast<const f32x4*>(a.rc + g) : f32x4{};
+  if (grp == 1) return;
+  // the two remote states at their common max (dense_fwd_merge's
+  // combination): weights dr_g 2^{2(m_g - m)} of the groups' means
+  const float m1 = xrow[0][lrow], zs1 = xrow[1][lrow], dr1 = xrow[2][lrow];
+  const float mx = fmaxf(m_r, m1);
+  float zs = 0.f, w0 = 0.f, w1 = 0.f;
+  if (mx != kNegInf) {
+    const float e0 = fast_exp2(m_r - mx), e1 = fast_exp2(m1 - mx);
+    zs = zs_r * e0 + zs1 * e1;
+    w0 = dr * e0 * e0;
+    w1 = dr1 * e1 * e1;
+  }
+  const float drs = w0 + w1;
+  const float a0 = drs > 0.f ? w0 / drs : 0.f, a1 = drs > 0.f ? w1 / drs : 0.f;
+  float log_zr = zs > 0.f ? log_mass(mx, zs) : kNegInf;
+  float lr = drs > 0.f ? log_mass(mx, drs) - fast_log2(zs) * kLn2 : kNegInf;
+  const float zsum = zs_l + swap_halves(zs_l);
+  constexpr int RL = DP / 4;          // lanes per row, 4 floats each
+  constexpr int NIT = 32 * RL / 64;   // row-contiguous passes over the wave's 32 rows
+  const int row0 = qt * 128 + wg * 32;
+  if (a.fw0 != nullptr && !piece && threadIdx.x == 0) a.fflag[item] = split ? 1 : 0;
+  float xa0, xa1;  // per row: weights of the two remote means in the written remote part
+  float sf;        // scale of the staged acc
+  float* st8 = a.fstat + ((size_t)item * 128 + lrow) * 8;
+  if (split && piece == 0) {
+    // partial of piece 0: the joined remote mean
+    xa0 = 0.f;
+    xa1 = a1;
+    sf = dr > 0.f ? a0 / dr : 0.f;  // acc holds group 0's unnormalised remote sums
+    if (half == 0 && row_in) {
+      st8[0] = mx; st8[1] = zs; st8[2] = drs;
     }
+  } else if (split) {
+    // partial of piece 1: the joined remote mean (rc) and the local mean
+    xa0 = a0;
+    xa1 = a1;
+    sf = zsum > 0.f ? 1.f / zsum : 0.f;
+    if (half == 0 && row_in) {
+      st8[3] = mx; st8[4] = zs; st8[5] = drs; st8[6] = m_l; st8[7] = zsum;
+    }
+  } else {
+    const float dl = p >= 0 ? zsum : 0.f;
+    const float ll = p >= 0 ? log_mass(m_l, dl) : kNegInf;
+    if (p < 0) {
+      lr = kNegInf;
+      log_zr = kNegInf;
+    }
+    const float tot = logaddexp(lr, ll);
+    const float safe_total = tot == kNegInf ? 0.f : tot;
+    const float prem = lr == kNegInf ? 0.f : __expf(lr - safe_total);
+    const float ploc = ll == kNegInf ? 0.f : __expf(ll - safe_total);
+    xa0 = prem * a0;
+    xa1 = prem * a1;
+    sf = dl > 0.f ? ploc / dl : 0.f;
+    if (half == 0 && row_in) {
+      const int64_t si = ((int64_t)bi * a.Q + row) * H + hh;
+      a.pr[si] = prem;
+      a.zr[si] = log_zr;
+      a.z[si] = tot;
+    }
+  }
+  stage_acc(stage0, sf);
+  if (half == 0) {
+    xrow[0][lrow] = xa0;
+    xrow[1][lrow] = xa1;
+  }
+  // this wave's staged rows and weights (and its parked rc stores) are
+  // visible to all its lanes
+  __threadfence_block();
+  __builtin_amdgcn_wave_barrier();
+  typedef T T4 __attribute__((ext_vector_type(4)));
+  const int mode = split ? (piece ? 1 : 0) : 2;
+  float* fdst = split ? (piece == 0 ? a.fw0 : a.fw1) + (size_t)item * 128 * D : nullptr;
+  // every global load before the first store (the stores may alias in the
+  // compiler's view, which would serialise the round trips)
+  f32x4 mean[NIT];
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      const int r = (it * 64 + lane) / RL, c = ((it * 64 + lane) % RL) * 4;
-      if (row0 + r < a.Q) {
-        const int64_t g = (((int64_t)bi * a.Q + row0 + r) * H + hh) * D + c;
-        const float w = wst[r];
-        const f32x4 lv = *reinterpret_cast<const f32x4*>(lst + r * RLD + c);
-        f32x4 rc;
-        T4 o;
+  for (int it = 0; it < NIT; ++it) {
+    const int r = (it * 64 + lane) / RL, c = ((it * 64 + lane) % RL) * 4;
+    const int64_t gi = (((int64_t)bi * a.Q + row0 + r) * H + hh) * D + c;
+    mean[it] = (mode != 0 && row0 + r < a.Q) ? *reinterpret_cast<const f32x4*>(a.rc + gi) : f32x4{};
+  }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          rc[j] = mean[it][j] * w;
-          o[j] = from_float<T>(rc[j] + lv[j]);
-        }
-        *reinterpret_cast<f32x4*>(a.rc + g) = rc;
-        *reinterpret_cast<T4*>(reinterpret_cast<T*>(a.out) + g) = o;
-      }
+  for (int it = 0; it < NIT; ++it) {
+    const int r = (it * 64 + lane) / RL, c = ((it * 64 + lane) % RL) * 4;
+    if (row0 + r >= a.Q) continue;
+    const int64_t gi = (((int64_t)bi * a.Q + row0 + r) * H + hh) * D + c;
+    const f32x4 s0 = *reinterpret_cast<const f32x4*>(stage0 + sidx(r, c));
+    const f32x4 s1 = *reinterpret_cast<const f32x4*>(stage1 + sidx(r, c));
+    const float x0 = xrow[0][wg * 32 + r], x1 = xrow[1][wg * 32 + r];
+    const f32x4 rem = mean[it] * x0 + s1 * x1;  // the remote part (piece 0: group 1's share)
+    if (mode == 0) {
+      *reinterpret_cast<f32x4*>(fdst + (int64_t)(wg * 32 + r) * D + c) = s0 + rem;
+    } else if (mode == 1) {
+      *reinterpret_cast<f32x4*>(a.rc + gi) = rem;
+      *reinterpret_cast<f32x4*>(fdst + (int64_t)(wg * 32 + r) * D + c) = s0;
+    } else {
+      T4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = from_float<T>(rem[j] + s0[j]);
+      *reinterpret_cast<f32x4*>(a.rc + gi) = rem;
+      *reinterpret_cast<T4*>(reinterpret_cast<T*>(a.out) + gi) = o;
     }
   }
 }
@@ -683,9 +724,9 @@ static hipError_t launch_fast(const DenseArgs& args, hipStream_t stream) {
   dim3 grid((unsigned)(per_head * a.B * a.H));
   auto go = [&]<int LOGB>() {
     note_launch((const void*)&dense_fwd_fast_kernel<T, DP, LOGB>,
-                {"dense_fwd_fast", dtype_code<T>(), DP, 1 << LOGB, 128, 128, 4, 2, grid.x,
+                {"dense_fwd_fast", dtype_code<T>(), DP, 1 << LOGB, 128, 128, 8, 2, grid.x,
                  a.f_pair ? "pair" : (a.fw0 ? "slot" : "grid")});
-    hipLaunchKernelGGL((dense_fwd_fast_kernel<T, DP, LOGB>), grid, dim3(256), 0, stream, a, n_qtiles);
+    hipLaunchKernelGGL((dense_fwd_fast_kernel<T, DP, LOGB>), grid, dim3(512), 0, stream, a, n_qtiles);
   };
   switch (a.logb) {
     case 1: go.template operator()<1>(); break;

@@ -152,6 +152,16 @@ struct OpMax {
   static __device__ __forceinline__ float other(float x) { return other_half(x); }
 };
 
+// Op over the 16 registers of a C tile as a balanced tree.
+template <typename Op> __device__ __forceinline__ float tree16(const f32x16& x) {
+  float a[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = Op::f(x[2 * i], x[2 * i + 1]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = Op::f(a[2 * i], a[2 * i + 1]);
+  return Op::f(Op::f(a[0], a[1]), Op::f(a[2], a[3]));
+}
+
 template <int NST, int LOGB, typename Op = OpAdd>
 __device__ __forceinline__ void block_sums(const f32x16 (&x)[NST], float (&blk)[NST][8]) {
   if constexpr ((1 << LOGB) > 32 * NST) {
@@ -263,13 +273,22 @@ template <typename T, int DP, int NWAVES> struct Stager {
   static_assert(RPI % kSwzPeriod == 0, "a slab must keep the swizzle phase");
   const char* base;
   uint32_t row_bytes;
-  int nrows, r_lane;
+  int nrows, r_lane, wave;
   uint32_t voff;  // r_lane * row_bytes + 16 * swizzled chunk
-  __device__ __forceinline__ Stager(const T* base_, int64_t stride, int nrows_) {
-    const int p = (int)threadIdx.x;
+  // tid: this thread's index among the NWAVES * 64 threads that stage (the
+  // workgroup, or one group of its waves)
+  __device__ __forceinline__ Stager(const T* base_, int64_t stride, int nrows_, int tid = (int)threadIdx.x) {
+    const int p = tid;
+    // wave-uniform (scalar) so that the LDS destinations are scalar too
+    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     r_lane = p / CPR;
     const int chunk = (p % CPR) ^ swz<DP>(r_lane);
-    base = reinterpret_cast<const char*>(base_);
+    // the matrix base in SGPRs: every copy then takes the scalar-base form
+    // (SGPR pair + 32-bit VGPR offset, no 64-bit address arithmetic)
+    const uint64_t b64 = reinterpret_cast<uint64_t>(base_);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b64);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b64 >> 32));
+    base = reinterpret_cast<const char*>(((uint64_t)hi << 32) | lo);
     row_bytes = (uint32_t)(stride * (int64_t)sizeof(T));
     nrows = nrows_;
     voff = (uint32_t)r_lane * row_bytes + (uint32_t)chunk * 16u;
@@ -277,8 +296,6 @@ template <typename T, int DP, int NWAVES> struct Stager {
   template <int ROWS>
   __device__ __forceinline__ void stage(T* lds, int r0) const {
     static_assert(ROWS % RPI == 0, "tile must split into whole slabs");
-    // wave-uniform (scalar) so that the LDS destinations are scalar too
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (r0 + ROWS <= nrows) {
       const uint32_t s0 = (uint32_t)r0 * row_bytes, slab = (uint32_t)RPI * row_bytes;
 #pragma unroll
@@ -389,6 +406,141 @@ __device__ __forceinline__ void mfma_phase_overlap(Load&& load, Mfma&& mma, Slic
       [&]<int... K>(std::integer_sequence<int, K...>) {
         (slice.template operator()<g * NS / C + K>(), ...);
       }(std::make_integer_sequence<int, (g + 1) * NS / C - g * NS / C>{});
+    }(), ...);
+  }(std::make_integer_sequence<int, C>{});
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// ---------------------------------------------------------------------------
+// 16x16x32 MFMA layout helpers (v_mfma_f32_16x16x32_{bf16,f16}): a C tile
+// of S^T = K Q^T puts query row l%16 in lane l and keys 4*(l/16)+r
+// (r = 0..3) of a 16-key subtile in its registers, so a row's values are
+// spread over the four 16-lane rows of the wave (lanes i, i+16, i+32, i+48).
+
+// Op over lanes i and i^16 (16-lane rows 0/1 and 2/3), result in both: one
+// v_permlane16_swap returns the pair's two values in its two outputs.
+template <typename Op> __device__ __forceinline__ float reduce_pair16(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return Op::f(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// Op over lanes i and i^32.
+template <typename Op> __device__ __forceinline__ float reduce_pair32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return Op::f(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// Op over the four 16-lane rows (a query row's lanes), result in all four.
+template <typename Op> __device__ __forceinline__ float reduce_rows4(float x) {
+  return reduce_pair32<Op>(reduce_pair16<Op>(x));
+}
+
+template <typename Op> __device__ __forceinline__ float op4(const f32x4& x) {
+  return Op::f(Op::f(x[0], x[1]), Op::f(x[2], x[3]));
+}
+
+// Per-(row, key block) reductions of NSUB 16-key C subtiles (block size
+// 2^LOGB, the subtiles hold whole blocks). blk[t][s] receives the total of
+// block slot s of subtile t in every lane that holds part of the block:
+// block size 2 has two slots per subtile (registers 0-1, 2-3), larger sizes
+// one. Blocks of 32..128 keys span 2..8 subtiles; each of them gets the
+// block total.
+template <int LOGB> __device__ __forceinline__ constexpr int slot16(int r) { return LOGB == 1 ? (r >> 1) : 0; }
+template <int LOGB> struct Slots16 { static constexpr int n = LOGB == 1 ? 2 : 1; };
+
+template <int NSUB, int LOGB, typename Op = OpAdd>
+__device__ __forceinline__ void block_sums16(const f32x4 (&x)[NSUB], float (&blk)[NSUB][2]) {
+  if constexpr (LOGB == 1) {
+#pragma unroll
+    for (int t = 0; t < NSUB; ++t) {
+      blk[t][0] = Op::f(x[t][0], x[t][1]);
+      blk[t][1] = Op::f(x[t][2], x[t][3]);
+    }
+  } else if constexpr (LOGB == 2) {
+#pragma unroll
+    for (int t = 0; t < NSUB; ++t) blk[t][0] = op4<Op>(x[t]);
+  } else if constexpr (LOGB == 3) {
+#pragma unroll
+    for (int t = 0; t < NSUB; ++t) blk[t][0] = reduce_pair16<Op>(op4<Op>(x[t]));
+  } else if constexpr (LOGB == 4) {
+#pragma unroll
+    for (int t = 0; t < NSUB; ++t) blk[t][0] = reduce_rows4<Op>(op4<Op>(x[t]));
+  } else {
+    constexpr int G = (1 << LOGB) / 16 < NSUB ? (1 << LOGB) / 16 : NSUB;
+#pragma unroll
+    for (int t0 = 0; t0 < NSUB; t0 += G) {
+      float tot = op4<Op>(x[t0]);
+#pragma unroll
+      for (int t = t0 + 1; t < t0 + G; ++t) tot = Op::f(tot, op4<Op>(x[t]));
+      tot = reduce_rows4<Op>(tot);
+#pragma unroll
+      for (int t = t0; t < t0 + G; ++t) blk[t][0] = tot;
+    }
+  }
+}
+
+// block_sums16 for blocks of 4+ keys from the subtiles' in-lane partials
+// part[t] (the op over the lane's four values of subtile t).
+template <int NSUB, int LOGB, typename Op = OpAdd>
+__device__ __forceinline__ void block_sums16_from(const float (&part)[NSUB], float (&blk)[NSUB][2]) {
+  static_assert(LOGB >= 2, "blocks of 2 keys need the single values");
+  if constexpr (LOGB == 2) {
+#pragma unroll
+    for (int t = 0; t < NSUB; ++t) blk[t][0] = part[t];
+  } else if constexpr (LOGB == 3) {
+#pragma unroll
+    for (int t = 0; t < NSUB; ++t) blk[t][0] = reduce_pair16<Op>(part[t]);
+  } else if constexpr (LOGB == 4) {
+#pragma unroll
+    for (int t = 0; t < NSUB; ++t) blk[t][0] = reduce_rows4<Op>(part[t]);
+  } else {
+    constexpr int G = (1 << LOGB) / 16 < NSUB ? (1 << LOGB) / 16 : NSUB;
+#pragma unroll
+    for (int t0 = 0; t0 < NSUB; t0 += G) {
+      float tot = part[t0];
+#pragma unroll
+      for (int t = t0 + 1; t < t0 + G; ++t) tot = Op::f(tot, part[t]);
+      tot = reduce_rows4<Op>(tot);
+#pragma unroll
+      for (int t = t0; t < t0 + G; ++t) blk[t][0] = tot;
+    }
+  }
+}
+
+// Whether block slot s of subtile t counts in a lane of 16-lane row g when
+// a per-row sum over blocks is later reduced over the four rows (each block
+// once).
+template <int LOGB> __device__ __forceinline__ bool owns16(int t, int g) {
+  if constexpr (LOGB <= 2) return true;
+  else if constexpr (LOGB == 3) return (g & 1) == 0;
+  else if constexpr (LOGB == 4) return g == 0;
+  else return g == 0 && (t % ((1 << LOGB) / 16)) == 0;
+}
+
+// An MFMA phase of N products in chunks of L whose A operands are read from
+// LDS (the first NR2 products two reads each, e.g. transposed V fragments,
+// the rest one): wait for the reads in flight, issue the reads of chunk g+1,
+// then the L MFMAs of chunk g (see mfma_phase).
+template <int N, int L, int NR2, typename Load, typename Mfma>
+__device__ __forceinline__ void mfma_chunks(Load&& load, Mfma&& mma) {
+  static_assert(N % L == 0 && NR2 % L == 0, "phase must split into whole chunks");
+  constexpr int C = N / L;
+  typedef decltype(load(0)) F;
+  F buf[2][L];
+#pragma unroll
+  for (int i = 0; i < L; ++i) buf[0][i] = load(i);
+  [&]<int... G>(std::integer_sequence<int, G...>) {
+    ([&] {
+      constexpr int g = G;
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt untouched
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (g + 1 < C) {
+#pragma unroll
+        for (int i = 0; i < L; ++i) buf[(g + 1) & 1][i] = load((g + 1) * L + i);
+      }
+#pragma unroll
+      for (int i = 0; i < L; ++i) mma(g * L + i, buf[g & 1][i]);
+      if constexpr (g + 1 < C) __builtin_amdgcn_sched_group_barrier(0x100, L * ((g + 1) * L < NR2 ? 2 : 1), 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, L, 0);
     }(), ...);
   }(std::make_integer_sequence<int, C>{});
   __builtin_amdgcn_sched_barrier(0);
