@@ -248,38 +248,75 @@ def bench_decode(model, torch, context=131072, queries=16):
             "decode_ms_mean": sum(per) / len(per), "decode_ms_median": statistics.median(per)}
 
 
-def cpu_baseline(budget_s, torch):
-    """The oracle's eager dense forward+backward (the reference's CPU eager
-    path, st/tools/benchmark.py:27-43) on a bounded sample of cfg2: one of the
-    eight heads, fp32, all host cores."""
-    from exploration_amd.workloads import dense_inputs, dense_flops
-    from oracle import dense as od
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
-    q, k, v, pos, do = dense_inputs(1, 4096, 4096, 1, 128, torch.float32, seed=0, scale=1 / math.sqrt(128))
-    q, k, v = (t.requires_grad_() for t in (q, k, v))
-    flops = dense_flops(pos, 4096, 1, 128)
 
-    def run():
-        q.grad = k.grad = v.grad = None
-        out = od.eager_attention(q, k, v, pos, 128)
-        out.backward(do)
-
-    t0 = time.perf_counter()
-    run()  # warmup
-    first = time.perf_counter() - t0
-    reps = max(1, min(10, int(budget_s / max(first, 1e-3)) - 1))
+def _median_seconds(run, warmup, reps):
+    """perf_counter median of ``reps`` runs after ``warmup`` untimed ones
+    (the reference harness defaults are 3 and 10, st/tools/benchmark.py:66-67)."""
+    for _ in range(warmup):
+        run()
     times = []
     for _ in range(reps):
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    return {"value": flops / med / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": f"cfg2 restricted to 1 of 8 heads (B1 H1 N=Q=4096 D128 b128 fp32, causal), "
-                      f"oracle eager forward+backward, median of {reps} after 1 warmup",
-            "seconds_per_step": med}
+    return statistics.median(times)
+
+
+def cpu_baseline(budget_s, torch):
+    """The oracle's restatement of the reference's CPU paths, timed on this
+    host's cores: cfg1 (B2 H4 N=Q=512 D64 b64, fp32, arange positions, seed 0)
+    forward+backward in the eager Q x N form (st/tools/benchmark.py:27-43; the
+    reported value) and in the bounded-memory chunked form with q_chunk 32 and
+    kv_chunk 1024 (st/ops/attention.py:51-139), then one of cfg2's eight heads
+    (N=Q=4096 D128 b128, fp32) in the eager form, if the budget allows."""
+    from exploration_amd.workloads import CFG1, dense_config, dense_flops, dense_inputs
+    from oracle import dense as od
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+
+    def fwd_bwd(q, k, v, do, forward):
+        def run():
+            qg, kg, vg = (t.detach().requires_grad_() for t in (q, k, v))
+            forward(qg, kg, vg).backward(do)
+        return run
+
+    q, k, v, pos, do, b = dense_config(CFG1)
+    flops = dense_flops(pos, CFG1["length"], CFG1["heads"], CFG1["dim"])
+    t0 = time.perf_counter()
+    eager = _median_seconds(fwd_bwd(q, k, v, do, lambda a, c, e: od.eager_attention(a, c, e, pos, b)), 3, 10)
+    chunked = _median_seconds(
+        fwd_bwd(q, k, v, do, lambda a, c, e: od.chunked_attention(a, c, e, pos, b, 32, 1024)), 3, 10)
+    line = {"value": flops / eager / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "cpu": _cpu_model(),
+            "sample": "cfg1: B2 H4 N=Q=512 D64 b64 fp32, arange positions, q/k/v/dO ~ N(0,1) seed 0; "
+                      "oracle eager forward+backward (Q x N form), 3 warmups, median of 10",
+            "seconds_per_step": eager, "flop_per_step": flops,
+            "chunked": {"value": flops / chunked / 1e12, "unit": "TFLOP/s", "seconds_per_step": chunked,
+                        "q_chunk": 32, "kv_chunk": 1024,
+                        "sample": "cfg1, oracle chunked bounded-memory forward+backward, 3 warmups, median of 10"}}
+    if time.perf_counter() - t0 < budget_s:
+        q, k, v, pos, do = dense_inputs(1, 4096, 4096, 1, 128, torch.float32, seed=0, scale=1 / math.sqrt(128))
+        flops2 = dense_flops(pos, 4096, 1, 128)
+        run = fwd_bwd(q, k, v, do, lambda a, c, e: od.eager_attention(a, c, e, pos, 128))
+        first = time.perf_counter()
+        run()
+        reps = max(1, min(10, int((budget_s - (time.perf_counter() - t0)) / max(time.perf_counter() - first, 1e-3))))
+        sec = _median_seconds(run, 2, reps)
+        line["cfg2_one_head"] = {"value": flops2 / sec / 1e12, "unit": "TFLOP/s", "seconds_per_step": sec,
+                                 "sample": f"cfg2 restricted to 1 of 8 heads (B1 H1 N=Q=4096 D128 b128 fp32, "
+                                           f"causal), oracle eager forward+backward, 3 warmups, median of {reps}"}
+    return line
 
 
 def main():

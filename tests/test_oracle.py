@@ -53,6 +53,55 @@ def test_three_forms_agree_and_gradients_match(n, b):
         torch.testing.assert_close(x, e, atol=1e-10, rtol=1e-9)
 
 
+@pytest.mark.parametrize("n,b,q_chunk,kv_chunk", [
+    (1, 2, 1, 1), (17, 4, 3, 8), (33, 8, 5, 13), (33, 8, 32, 1024), (70, 16, 2, 16), (70, 16, 7, 48)])
+def test_chunked_form_matches_stats_and_explicit_backward(n, b, q_chunk, kv_chunk):
+    """The bounded-memory form (st/ops/attention.py:51-139) at several tile
+    sizes, including tiles smaller than a block (rounded up to one block),
+    tiles that cut the ragged last block and padding rows: its five saved
+    statistics equal forward_stats, its gradients equal backward_explicit and
+    autograd through the loop form."""
+    g = _gen(77 + n)
+    q = _rand((2, 6, 3, 8), g, requires_grad=True)
+    k = _rand((2, n, 3, 8), g, requires_grad=True)
+    v = _rand((2, n, 3, 8), g, requires_grad=True)
+    pos = torch.tensor([[n - 1, 0, -1, n // 2, min(2 * b, n - 1), n - 1],
+                        [-1, n // 3, n - 1, 0, n - 1, max(0, n - b)]])
+    ref = od.forward_stats(q.detach(), k.detach(), v.detach(), pos, b)
+    got = od.chunked_forward(q.detach(), k.detach(), v.detach(), pos, b, q_chunk, kv_chunk)
+    for name, x, e in zip(("out", "rc", "pr", "zr", "z"), got, ref):
+        torch.testing.assert_close(x, e, atol=1e-12, rtol=1e-11, msg=name)
+    probe = _rand(q.shape, g)
+    out = od.chunked_attention(q, k, v, pos, b, q_chunk, kv_chunk)
+    gc = torch.autograd.grad((out * probe).sum(), (q, k, v))
+    gx = od.backward_explicit(q.detach(), k.detach(), v.detach(), pos, b, probe, ref)
+    gl = torch.autograd.grad((od.loop_attention(q, k, v, pos, b) * probe).sum(), (q, k, v))
+    for c, x, l in zip(gc, gx, gl):
+        torch.testing.assert_close(c, x, atol=1e-11, rtol=1e-10)
+        torch.testing.assert_close(c, l, atol=1e-10, rtol=1e-9)
+
+
+def test_chunked_form_fp32_cfg1_tiles():
+    """cfg1 shape (B2 H4 N=Q=512 D64 b64, fp32, arange positions) at the
+    reference's default tiles q_chunk=32, kv_chunk=1024 and at kv_chunk=128
+    (four key tiles per row): within fp32 rounding of the float64 eager form."""
+    g = _gen(0)
+    q, k, v, do = (torch.randn(2, 512, 4, 64, generator=g) for _ in range(4))
+    pos = torch.arange(512).expand(2, 512)
+    want = od.eager_attention(q.double(), k.double(), v.double(), pos, 64)
+    qd, kd, vd = (t.double() for t in (q, k, v))
+    saved = od.forward_stats(qd, kd, vd, pos, 64)
+    dwant = od.backward_explicit(qd, kd, vd, pos, 64, do.double(), saved)
+    for kv_chunk in (1024, 128):
+        qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+        out = od.chunked_attention(qg, kg, vg, pos, 64, 32, kv_chunk)
+        assert out.dtype == torch.float32
+        torch.testing.assert_close(out.double(), want, atol=1e-5, rtol=1e-5)
+        out.backward(do)
+        for got, e in zip((qg.grad, kg.grad, vg.grad), dwant):
+            torch.testing.assert_close(got.double(), e, atol=2e-5, rtol=1e-5)
+
+
 def test_gate_gradient_finite_difference():
     """tests/test_attention.py:65-73 case, through both gate terms."""
     g = _gen(4)
