@@ -41,12 +41,14 @@ SIGNATURES = {
     "st_sparse_noalloc_scratch_bytes": (_sz, []),
     "st_sparse_fwd_noalloc": (ctypes.c_int, [ctypes.c_int] + [_i64] * 6 + [_p, _i64p, _p, _p, _i32p]
                               + [_i64] * 4 + [_p, _i64p, _f32p, _f32p, _f32p, _p]),
+    "st_paged_kv_write": (ctypes.c_int, [ctypes.c_int] + [_i64] * 4 + [_p, _p, _i32p] + [_i64] * 3
+                          + [_p, _p, _i64, _p]),
     "st_halo_supported": (ctypes.c_int, [ctypes.c_int, _i64, _i64]),
     "st_halo_attn_fwd": (ctypes.c_int, [ctypes.c_int] + [_i64] * 8 + [_p, _f32p, _f32p, _p, _p]),
     "st_halo_attn_bwd": (ctypes.c_int, [ctypes.c_int] + [_i64] * 8 + [_p, _f32p, _f32p, _p, _p, _p, _p]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 _lib = None
 
 

@@ -452,6 +452,30 @@ int st_sparse_fwd(int dtype, int64_t batch, int64_t queries, int64_t heads, int6
 }  // extern "C"
 
 // ---------------------------------------------------------------------------
+// paged KV cache write
+
+int st_paged_kv_write(int dtype, int64_t batch, int64_t tokens, int64_t heads, int64_t head_dim,
+                      const void* k, const void* v, const int32_t* page_table, int64_t page_tokens,
+                      int64_t pages_per_seq, int64_t first_token, void* k_pool, void* v_pool,
+                      int64_t pool_pages, void* stream) {
+  if (int r = check_dtype(dtype)) return r;
+  if (batch < 1 || tokens < 1 || heads < 1 || head_dim < 1 || page_tokens < 1 || pages_per_seq < 1 ||
+      pool_pages < 1)
+    return fail(ST_EINVAL, "st_paged_kv_write: dimensions must be positive");
+  if (first_token < 0 || first_token + tokens > pages_per_seq * page_tokens)
+    return fail(ST_EINVAL, "KV write outside owned shard");
+  if (batch > 65535 || heads * head_dim > (int64_t(1) << 24))
+    return fail(ST_EUNSUPPORTED, "st_paged_kv_write: batch above 65535 or heads*head_dim above 2^24");
+  if (!k || !v || !page_table || !k_pool || !v_pool) return fail(ST_EINVAL, "st_paged_kv_write: null pointer");
+  st::PagedWrite w{};
+  w.k = k; w.v = v; w.k_pool = k_pool; w.v_pool = v_pool; w.page_table = page_table;
+  w.batch = batch; w.tokens = tokens; w.first_token = first_token; w.page_tokens = page_tokens;
+  w.pages_per_seq = pages_per_seq; w.pool_pages = pool_pages;
+  w.heads = (int)heads; w.head_dim = (int)head_dim; w.dtype = dtype;
+  w.row_bytes = head_dim * (dtype == ST_DTYPE_F32 ? 4 : 2);
+  return launched(st::launch_paged_write(w, as_stream(stream)), "st_paged_kv_write");
+}
+
 // local-block window attention
 
 static int fill_halo(st::HaloArgs& a, const char* who, int dtype, int64_t batch, int64_t groups, int64_t block_size,

@@ -43,6 +43,22 @@ inline int sparse_dp(int d) { return d <= 64 ? 64 : (d <= 128 ? 128 : 256); }
 constexpr int kPopSlotsPerGroup = 4;  // blocks read by one workgroup
 inline int64_t sparse_chunks(int topk) { return (topk + 2 + kPopSlotsPerGroup - 1) / kPopSlotsPerGroup; }
 
+// Copy of k, v [batch, tokens, H, D] into pools [pool_pages, H, page_tokens,
+// D] through a page table (range-relative token first_token + t of batch row
+// b goes to page page_table[b * pages_per_seq + tok / page_tokens]).
+struct PagedWrite {
+  const void* k;
+  const void* v;
+  void* k_pool;
+  void* v_pool;
+  const int32_t* page_table;
+  int64_t batch, tokens, first_token, page_tokens, pages_per_seq, pool_pages;
+  int heads, head_dim, dtype;
+  int64_t row_bytes;  // head_dim * element bytes
+};
+
+hipError_t launch_paged_write(const PagedWrite& w, hipStream_t stream);
+
 hipError_t launch_sparse_scores(int dtype, const SparseArgs& a, hipStream_t stream);
 hipError_t launch_sparse_select(int64_t rows, int64_t n_blocks, int topk, int64_t id_base,
                                 const float* scores, int64_t* ids, float* top, float* log_zr,

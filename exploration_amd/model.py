@@ -16,6 +16,7 @@ identity here. The reference's differentiable sparse plumbing
 shipped: a gradient-enabled sparse forward raises ``ValueError``.
 """
 import math
+import re
 from dataclasses import asdict, dataclass, fields
 from numbers import Integral
 
@@ -76,32 +77,39 @@ class ExecutionConfig:
             raise ValueError("backend must be auto, torch, triton or hip")
 
 
+_ARCH_ITEM = re.compile(r"\((?P<shared>[^()]*)\)x(?P<repeat>.*)|(?P<kind>[^()x]*)(?:x(?P<count>.*))?", re.S)
+
+
 def parse_arch(arch):
-    """``'Lx2,(G)x4'`` -> ``[(kind, count, shared), ...]`` (``stack.py:75-106``):
-    L = local halo encoder block, G = global read round; ``XxN`` repeats with
-    independent weights, ``(X)xN`` cycles one shared layer; every L precedes
-    every G."""
+    """Layer plan of a Stack model, ``'Lx2,(G)x4'`` -> ``[(kind, count,
+    shared), ...]`` in application order (the reference's grammar,
+    ``st/models/stack.py:75-106``).
+
+    Items are comma separated. ``L`` is a local halo encoder block, ``G`` a
+    global read round. ``XxN`` stacks N layers with their own weights,
+    ``(X)xN`` applies one shared layer N times, bare ``X`` is one layer. N is
+    a positive decimal integer (an empty ``Xx`` is rejected). The model
+    encodes, then reads: no ``L`` item may follow a ``G`` item."""
     if not isinstance(arch, str) or not arch.strip():
         raise ValueError("arch must be a nonempty spec like 'Lx2,G'")
-    spec = []
-    for raw in arch.split(","):
-        item = raw.strip()
-        shared = item.startswith("(")
-        if shared:
-            kind, sep, count = item[1:].partition(")x")
-            if not sep:
+    spec, reading = [], False
+    for item in (part.strip() for part in arch.split(",")):
+        m = _ARCH_ITEM.fullmatch(item)
+        if m is None or (m["kind"] is None and m["shared"] is None):
+            if item.startswith("("):
                 raise ValueError(f"shared layers must look like '(X)xN': {item!r}")
-        else:
-            kind, _, count = item.partition("x")
-            count = count or "1"
+            raise ValueError(f"unknown layer kind in arch item {item!r} (want L or G)")
+        shared = m["shared"] is not None
+        kind = m["shared"] if shared else m["kind"]
+        count = m["repeat"] if shared else ("1" if m["count"] is None else m["count"])
         if kind not in ("L", "G"):
             raise ValueError(f"unknown layer kind in arch item {item!r} (want L or G)")
-        if not count.isdigit() or int(count) < 1:
+        if not re.fullmatch(r"[0-9]+", count) or int(count) == 0:
             raise ValueError(f"repeat count must be a positive integer in {item!r}")
+        if kind == "L" and reading:
+            raise ValueError("all L layers must precede all G layers (encode -> read)")
+        reading = reading or kind == "G"
         spec.append((kind, int(count), shared))
-    kinds = [k for k, _, _ in spec]
-    if "L" in kinds and "G" in kinds and kinds.index("G") < len(kinds) - 1 - kinds[::-1].index("L"):
-        raise ValueError("all L layers must precede all G layers (encode -> read)")
     return spec
 
 
@@ -425,8 +433,10 @@ class StackModel(nn.Module):
         # supervised positions of each row in increasing order, padded with n:
         # a row prefix sum gives each one its slot, a scatter places it (the
         # unsupervised ones all land in a discarded extra column). No sort and
-        # no boolean selection: those run decoupled look-back scans, whose
-        # spin-waits have hung in replays of a captured step.
+        # no boolean selection: those run rocprim look-back scans that clear
+        # their counters with a memset, and a captured memset node has not
+        # re-run reliably on replays here (a replayed partition kernel then
+        # wrote out of bounds: a memory aperture fault).
         idx = torch.arange(n, device=input_ids.device)[None].expand(batch, -1)
         # (a zero row keeps the prefix sum a per-row scan: one row alone goes
         # to the library's device-wide scan, which is a look-back scan)

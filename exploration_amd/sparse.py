@@ -98,6 +98,37 @@ class PagedKV:
         return self.page_table.shape[0]
 
     @classmethod
+    def empty(cls, batch, length, heads, dim, dtype, device, page_tokens=128, offset=0):
+        """A zero-filled cache for ``length`` tokens: ``batch * ceil(length /
+        page_tokens)`` pool pages, batch row ``b``'s logical pages at pool
+        pages ``b * pages ...`` in order. Fill it with ``write``."""
+        pages = -(-int(length) // page_tokens)
+        table = torch.arange(batch * pages, dtype=torch.int32, device=device).reshape(batch, pages)
+        k_pool = torch.zeros(batch * pages, heads, page_tokens, dim, dtype=dtype, device=device)
+        return cls(k_pool, torch.zeros_like(k_pool), table, length, offset)
+
+    def write(self, start, k, v):
+        """Store ``k, v [B, T, H, D]`` (device, the pool's dtype) at absolute
+        tokens ``[start, start + T)`` through the page table, in one kernel
+        on the current stream (``st_paged_kv_write``; the reference's
+        ``KVCache.write``, ``st/runtime/inference.py:45-52``)."""
+        lo = start - self.offset
+        if lo < 0 or lo + k.shape[1] > self.length:
+            raise ValueError("KV write outside owned shard")
+        pool = self.k_pool
+        if k.shape != v.shape or k.ndim != 4 or k.shape[0] != self.batch or k.shape[2] != pool.shape[1] \
+                or k.shape[3] != pool.shape[3]:
+            raise ValueError("expected k, v [B, T, H, D] matching the cache")
+        if k.dtype != pool.dtype or v.dtype != pool.dtype or k.device != pool.device or v.device != pool.device:
+            raise ValueError("k, v must have the cache's dtype and device")
+        lib = _lib.load()
+        k, v = k.contiguous(), v.contiguous()
+        _lib.check(lib.st_paged_kv_write(_lib.DTYPE_CODES[pool.dtype], k.shape[0], k.shape[1], k.shape[2],
+                                         k.shape[3], _lib.ptr(k), _lib.ptr(v), _lib.ptr(self.page_table),
+                                         self.page_tokens, self.page_table.shape[1], lo, _lib.ptr(pool),
+                                         _lib.ptr(self.v_pool), pool.shape[0], _lib.stream_of(k)), lib)
+
+    @classmethod
     def from_dense(cls, k, v, page_tokens, page_table=None, offset=0):
         """Build a paged cache from contiguous ``k, v [B, N, H, D]``. With
         ``page_table=None`` pages are laid out in order."""
@@ -236,6 +267,19 @@ def _sparse_host(q, cache, positions, b, topk, return_selection):
     return out
 
 
+def sparse_workspace_bytes(batch, queries, heads, head_dim, topk, n_blocks):
+    """Device workspace of one ``st_sparse_fwd`` call, as the library computes
+    it (``st_sparse_workspace_bytes``): the float32 block scores of every
+    row, then the read's float32 partials (``ceil((topk + 2) / 4)`` chunks of
+    ``Dp + 2`` floats per row, ``Dp`` = 64, 128 or 256), each rounded up to
+    256 bytes. Host arithmetic only, so planners can use it without a GPU."""
+    rows = batch * queries * heads
+    dp = 64 if head_dim <= 64 else (128 if head_dim <= 128 else 256)
+    chunks = (topk + 2 + 3) // 4
+    up = lambda x: (x + 255) // 256 * 256
+    return up(4 * rows * n_blocks) + up(4 * rows * chunks * (dp + 2))
+
+
 def _host_resident(cache):
     k, v = getattr(cache, "k", None), getattr(cache, "v", None)
     return (isinstance(k, torch.Tensor) and isinstance(v, torch.Tensor) and k.device.type == "cpu"
@@ -278,6 +322,8 @@ def sparse_attention(q, cache, positions, block_size, topk, backend="auto", grou
     b = block_size
     if backend not in BACKENDS:
         raise ValueError(f"unknown attention backend {backend!r}")
+    if isinstance(getattr(cache, "paged", None), PagedKV):
+        cache = cache.paged  # an inference session's HBM-tier cache
     if topk < 1 or score_page_tokens < b or cache.page_tokens % b or cache.offset % b:
         raise ValueError("topk positive; cache pages/offset must be block aligned")
     if backend == "torch":

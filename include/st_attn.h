@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ST_ABI_VERSION 4
+#define ST_ABI_VERSION 5
 
 #define ST_DTYPE_F32 0
 #define ST_DTYPE_F16 1
@@ -177,6 +177,21 @@ int st_sparse_fwd_noalloc(int dtype, int64_t batch, int64_t queries, int64_t hea
                           const void* k, const void* v, const int32_t* page_table, int64_t page_tokens,
                           int64_t pages_per_seq, int64_t n_tokens, int64_t token_offset, void* out,
                           int64_t* ids, float* top_scores, float* log_zr, float* lse, void* stream);
+
+/* Write of K and V rows k, v [batch, tokens, H, D] into a paged cache
+ * k_pool, v_pool [pool_pages, H, page_tokens, D]: token t of batch row b
+ * (range-relative token first_token + t) lands in pool page
+ * page_table[b * pages_per_seq + (first_token + t) / page_tokens], row
+ * (first_token + t) % page_tokens. page_table holds batch * pages_per_seq
+ * int32 entries; an entry outside [0, pool_pages) is skipped (nothing is
+ * written for its tokens), so a bad table cannot write outside the pools.
+ * Replaces KVCache.write (st/runtime/inference.py:45-52), which copies into
+ * a contiguous [B, N, H, D] slab; the paged pool is what st_sparse_fwd
+ * reads. */
+int st_paged_kv_write(int dtype, int64_t batch, int64_t tokens, int64_t heads, int64_t head_dim,
+                      const void* k, const void* v, const int32_t* page_table, int64_t page_tokens,
+                      int64_t pages_per_seq, int64_t first_token, void* k_pool, void* v_pool,
+                      int64_t pool_pages, void* stream);
 
 /* Two-block window attention of the model's local blocks (no st.ops
  * counterpart: the reference computes it with torch's scaled dot-product

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in declared_functions():
         assert hasattr(lib, name), f"{name} missing from libst_attn.so"
-    assert lib.st_abi_version() == 4
+    assert lib.st_abi_version() == 5
     assert lib.st_launch_report(None, 0) >= 3  # "[]" and its NUL at least
     assert lib.st_last_error() == b""
 
@@ -90,6 +90,33 @@ def test_argument_errors_map_to_value_error():
     # fp32 head_dim 17 (generic kernels, no workspace of their own) at 24:
     # q, k, v, out and rc copies
     assert lib.st_dense_fwd_workspace_bytes(0, 1, 3, 3, 1, 17, 4) == 5 * pad(3 * 24 * 4)
+
+
+def test_workspace_size_mirror_matches_the_library():
+    """The planner's host-side workspace formula equals the library's."""
+    from exploration_amd.sparse import sparse_workspace_bytes
+    lib = _lib.load()
+    for shape in [(1, 16, 16, 64, 64, 8192), (1, 16, 8, 128, 64, 8192), (2, 3, 5, 40, 7, 100),
+                  (1, 1, 1, 256, 1, 1), (3, 17, 4, 200, 128, 0)]:
+        assert sparse_workspace_bytes(*shape) == lib.st_sparse_workspace_bytes(*shape), shape
+
+
+def test_paged_write_argument_checks():
+    """st_paged_kv_write rejects writes past the table's pages and null
+    pointers on the host, before any launch."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)  # never dereferenced: every call below fails its checks first
+    args = dict(dtype=2, batch=1, tokens=100, heads=2, head_dim=64, k=p, v=p, table=p, page_tokens=128,
+                pages_per_seq=1, first=29, kp=p, vp=p, pool_pages=1, stream=None)
+    status = lib.st_paged_kv_write(*args.values())  # tokens 29..128: one past the single page
+    assert status == _lib.ST_EINVAL and b"outside owned shard" in lib.st_last_error()
+    args.update(first=0, k=None)
+    assert lib.st_paged_kv_write(*args.values()) == _lib.ST_EINVAL
+    assert b"null pointer" in lib.st_last_error()
+    args.update(k=p, tokens=0)
+    assert lib.st_paged_kv_write(*args.values()) == _lib.ST_EINVAL
+    args.update(tokens=1, dtype=9)
+    assert lib.st_paged_kv_write(*args.values()) == _lib.ST_EINVAL
 
 
 def test_noalloc_entry_point_rejects_problems_beyond_its_array():

@@ -14,18 +14,43 @@ from exploration_amd.inference import InferencePlan, KVCache, plan_inference
 
 
 def test_plan_chunks_stack_100m():
+    """stack_100m (dim 1024, H16 hd64, b16, top-64, FFN 4096, vocab 256), bf16,
+    one 131,072-token prompt on the pinned host tier, 256 MiB workspace."""
     m = M.build_model(M.STACK_100M, device="meta", dtype=torch.bfloat16)
     plan = plan_inference(m, 1, 131072, cache="cpu")
     ws = 256 << 20
     assert plan.cache == "cpu"
-    assert plan.cache_bytes == 2 * 131072 * 1024 * 2
-    # page: min(65536, ws / (2*1*1024*2)) = 65536; encoder: ws / (24*1024*2) = 5461 -> 4096
-    assert plan.page_tokens == min(65536, ws // (2 * 1024 * 2)) // 16 * 16 == 65536
-    assert plan.encoder_chunk == 4096
-    # query chunk: min(16, ws / (16 heads * 64 topk * 16 b * 4)); score tile: min(page, ws / (4*16*16*4))
-    assert plan.query_chunk == 16
-    assert plan.score_tokens == 65536
+    assert plan.cache_bytes == 2 * 131072 * 16 * 64 * 2
+    # encoder: (9*1024 + 2*4096) elements * 2 bytes = 34,816 B per token -> 7710 tokens fit,
+    # capped at the requested 4096 (a multiple of lcm(16, 128))
+    assert ws // ((9 * 1024 + 2 * 4096) * 2) == 7710 and plan.encoder_chunk == 4096
+    # one read of 16 queries: 8 MiB of scores (256 rows x 8192 blocks) + partials + outputs
+    read16 = 4 * 256 * 8192 + 4 * 256 * 17 * 66 + 256 * (12 * 64 + 4 + 64 * 2)
+    assert plan.query_chunk == 16 and plan.read_bytes == read16
     assert plan.head_chunk == 16
+    # score chunk: two device K buffers of 2,048 B per token -> 65,536 tokens
+    assert plan.score_tokens == plan.page_tokens == 65536
+    assert plan.pool_pages == 0
+
+
+def test_plan_small_workspace_clamps_every_chunk():
+    m = M.build_model(M.STACK_100M, device="meta", dtype=torch.bfloat16)
+    plan = plan_inference(m, 1, 131072, cache="cpu", workspace_mb=1)
+    assert plan.encoder_chunk == 128       # 30 tokens fit: one unit of 128
+    assert plan.query_chunk == 1           # two queries need 1 MiB of scores alone
+    assert plan.head_chunk == 1
+    assert plan.score_tokens == 256        # 1 MiB / (2 x 2,048 B)
+
+
+def test_available_host_memory_takes_the_cgroup_limit(monkeypatch):
+    import exploration_amd.inference as inf
+    monkeypatch.setattr(inf, "_meminfo_available", lambda: 10 << 30)
+    monkeypatch.setattr(inf, "_cgroup_room", lambda: 3 << 30)
+    assert inf.available_host_memory() == 3 << 30
+    monkeypatch.setattr(inf, "_cgroup_room", lambda: None)
+    assert inf.available_host_memory() == 10 << 30
+    monkeypatch.setattr(inf, "_meminfo_available", lambda: None)
+    assert inf.available_host_memory() is None
 
 
 def test_plan_rejects():

@@ -4,6 +4,8 @@ oracle (the product path has no CPU operator). Cases follow the reference's
 tests/test_stack_model.py (model(): vocab 31, dim 16, heads 2, b 2, topk 3,
 pos_chunk 3; arch parser cases; future perturbation and prefix invariance;
 the dense read at topk >= blocks against the per-position loop)."""
+import re
+
 import pytest
 import torch
 
@@ -25,10 +27,20 @@ def small(**overrides):
     return M.StackModel(**args)
 
 
-@pytest.mark.parametrize("bad", ["", "G,L", "Lx0", "X", "(L)x0", "(G)", "L,", "Lx2,(G)x", "L,Gx2,Lx1"])
+@pytest.mark.parametrize("bad", ["", "G,L", "Lx0", "X", "(L)x0", "(G)", "L,", "Lx2,(G)x", "L,Gx2,Lx1",
+                                 "Lx", "Lx2x3", "(L)x+1", "((L))x2", "L x2"])
 def test_arch_parser_rejects(bad):
     with pytest.raises(ValueError):
         small(arch=bad)
+
+
+def test_arch_parser_results_and_messages():
+    assert M.parse_arch(" Lx2 , (G)x3,G ") == [("L", 2, False), ("G", 3, True), ("G", 1, False)]
+    assert M.parse_arch("(L)x1") == [("L", 1, True)]
+    for bad, message in [("", "nonempty spec"), ("(G)", "'(X)xN'"), ("Q", "unknown layer kind"),
+                         ("Lx0", "positive integer"), ("G,L", "precede")]:
+        with pytest.raises(ValueError, match=re.escape(message)):
+            M.parse_arch(bad)
 
 
 @pytest.mark.parametrize("good,passes", [("L", 1), ("Lx2,G", 3), ("(L)x3,(G)x2", 5), ("Gx2", 2)])
