@@ -196,8 +196,11 @@ int st_dense_fwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_
     a.fw1 = reinterpret_cast<float*>(ws + plan.off_w1);
     a.fstat = reinterpret_cast<float*>(ws + plan.off_stat);
     a.fflag = reinterpret_cast<int*>(ws + plan.off_flag);
-    // a row tile longer than half the longest possible one runs as two pieces
-    a.f_split = (int)((keys + 127) / 128 + 1) / 2;
+    // a row tile longer than half the longest possible one runs as two
+    // pieces; with few row tiles, every tile of two or more key tiles runs
+    // as plan.pieces pieces
+    a.f_pieces = plan.pieces;
+    a.f_split = plan.pieces > 2 ? 1 : (int)((keys + 127) / 128 + 1) / 2;
   }
   a.B = (int)batch; a.Q = (int)queries; a.N = (int)keys; a.H = (int)heads; a.D = Dp;
   a.block = (int)block_size; a.logb = log2i(block_size);
@@ -272,8 +275,11 @@ int st_dense_bwd(int dtype, int64_t batch, int64_t queries, int64_t keys, int64_
     a.k_count = reinterpret_cast<int*>(ws + plan.off_kcnt);
     a.q_part = reinterpret_cast<float*>(ws + plan.off_qpart);
     a.k_part = reinterpret_cast<float*>(ws + plan.off_kpart);
-    // an item longer than half the longest possible one runs as two pieces
-    a.q_split = (plan.n_ktiles + 1) / 2;
+    // an item longer than half the longest possible one runs as two pieces;
+    // with few row tiles, every dQ item of two or more key tiles runs as
+    // plan.q_pieces pieces
+    a.q_pieces = plan.q_pieces;
+    a.q_split = plan.q_pieces > 2 ? 1 : (plan.n_ktiles + 1) / 2;
     a.k_split = (plan.n_rtiles + 1) / 2;
     a.Qp = plan.Qp;
     a.nblk = plan.nblk;

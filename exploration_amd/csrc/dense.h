@@ -35,18 +35,23 @@ struct DenseArgs {
   int* k_count;           // [B*H*n_ktiles] 1 if the dK/dV item was split
   float* q_part;          // dQ partials, [item][piece][wave][register][lane]
   float* k_part;          // dK/dV partials, same order
-  int q_split, k_split;   // items with more tiles than this run as two pieces
+  int q_split, k_split;   // items with more tiles than this run in pieces
+  int q_pieces;           // pieces of a split dQ item (2, or up to kMaxPieces for few items)
   int q_pair;             // dQ in pair mode (row tiles n-1-j and j share workgroups)
   int k_pair;             // dK/dV in pair mode (key tiles j and n-1-j)
-  // pipelined forward: a long row tile runs as two pieces whose partial
-  // results dense_fwd_merge combines (fw0 null: never). Slot mode splits a
-  // tile with more than f_split key tiles in halves; pair mode (f_pair) runs
-  // row tiles n-1-j and j as one pair of workgroups with equal tile counts.
-  float* fw0;             // [item][128 rows][D] remote mean of piece 0
-  float* fw1;             // [item][128 rows][D] local mean of piece 1
-  float* fstat;           // [item][128 rows][8] partial statistics
+  // pipelined forward: a long row tile runs as f_pieces pieces (consecutive
+  // ranges of its remote key tiles, the last piece also its local tiles)
+  // whose partial results dense_fwd_merge combines (fw0 null: never). Slot
+  // mode splits a tile with more than f_split key tiles; pair mode (f_pair,
+  // two pieces) runs row tiles n-1-j and j as one pair of workgroups with
+  // equal tile counts.
+  float* fw0;             // [piece < f_pieces-1][item][128 rows][D] remote means of the other pieces
+  float* fw1;             // [item][128 rows][D] local mean of the last piece
+  float* fstat;           // [item][128 rows][f_pieces + 1][4] per piece (max, row sum, sum of
+                          // squared block sums), then the local (max, row sum)
   int* fflag;             // [item] 1 if the item was split
   int f_split;
+  int f_pieces;
   int f_pair;
   int B, Q, N, H, D;
   int block, logb;
@@ -62,9 +67,21 @@ hipError_t launch_dense_fwd(int dtype, const DenseArgs& a, hipStream_t stream);
 // split-item partials, indexed by row tile.
 struct DenseFwdPlan {
   bool fast;
-  int n_qtiles;
+  int n_qtiles, pieces;
   size_t off_w1, off_stat, off_flag, total;
 };
+
+// Pieces a split work item runs as (2, 4 or 8): two when the items already
+// fill the chip twice over (MI355X: 256 compute units), else four or
+// kMaxPieces, so that a launch with few row tiles (a short chunk of queries
+// over a long key range) still spreads over every compute unit.
+constexpr int kMaxPieces = 8;
+constexpr int kPlanCUs = 256;
+inline int split_pieces(int64_t items) {
+  if (8 * items <= kPlanCUs) return 8;
+  if (4 * items <= kPlanCUs) return 4;
+  return 2;
+}
 DenseFwdPlan dense_fwd_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t H, int64_t D);
 // Pipelined forward for 16-bit inputs with head_dim 64 or 128.
 bool dense_fwd_fast_supported(int dtype, const DenseArgs& a);
@@ -76,7 +93,7 @@ hipError_t launch_dense_bwd(int dtype, const DenseArgs& a, hipStream_t stream);
 // when it applies (16-bit, head_dim 64/128, table within its size cap).
 struct DenseBwdPlan {
   bool fast;
-  int Qp, nblk, n_rtiles, n_qtiles, n_ktiles;
+  int Qp, nblk, n_rtiles, n_qtiles, n_ktiles, q_pieces;
   size_t off_rho, off_lim, off_tmin, off_tmax, off_tab, off_qcnt, off_kcnt, off_qpart, off_kpart, total;
 };
 DenseBwdPlan dense_bwd_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t H, int64_t D,

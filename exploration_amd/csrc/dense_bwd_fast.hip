@@ -45,6 +45,7 @@ constexpr int kKT = 128;       // keys per dK/dV workgroup and per dQ key tile
 constexpr int kQPieceCost = 3;
 constexpr int kKPieceCost = 4;
 constexpr int kRT = 64;        // query rows per dK/dV step / row-tile statistic
+constexpr int kFewRTiles = 8;  // dK/dV launches over at most this many row tiles run unsplit
 constexpr int kMaxRTiles = 2048;
 constexpr size_t kMaxTable = size_t(4) << 30;
 constexpr float kInf = __builtin_inff();
@@ -82,8 +83,10 @@ DenseBwdPlan dense_bwd_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t 
   p.off_qcnt = p.off_tab + align256(tab);
   p.off_kcnt = p.off_qcnt + align256(sizeof(int) * q_items);
   p.off_qpart = p.off_kcnt + align256(sizeof(int) * k_items);
-  // per item and piece: 128 rows (keys) x D floats (x2 for dK and dV)
-  p.off_kpart = p.off_qpart + align256(sizeof(float) * q_items * 2 * 128 * (size_t)D);
+  // per item and piece: 128 rows (keys) x D floats (x2 for dK and dV); dQ
+  // items run as more than two pieces when they are few
+  p.q_pieces = split_pieces((int64_t)q_items);
+  p.off_kpart = p.off_qpart + align256(sizeof(float) * q_items * p.q_pieces * 128 * (size_t)D);
   p.total = p.off_kpart + align256(sizeof(float) * k_items * 2 * 2 * 128 * (size_t)D);
   return p;
 }
@@ -216,11 +219,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     full = rg1 == 0x7fffffff ? 0 : rg1 / NT;
   };
 
-  // The job: row tile qt, key tiles [t0, t1). A split tile runs as two
-  // pieces (piece 0: [0, h), piece 1: [h, n)) whose dQ partials
-  // dense_bwd_merge adds. Slot mode (a.q_pair == 0): slot k < n_qtiles takes
-  // row tile n_qtiles-1-k whole or its first half, slot n_qtiles+k its
-  // second half (tiles longer than q_split are halved). Pair mode: row
+  // The job: row tile qt, key tiles [t0, t1). A split tile runs as pieces
+  // of consecutive key tiles whose dQ partials dense_bwd_merge adds. Slot
+  // mode (a.q_pair == 0): slot k takes piece k / n_qtiles of row tile
+  // n_qtiles-1-k % n_qtiles (tiles longer than q_split run as q_pieces
+  // pieces of ceil(n / q_pieces) key tiles; a piece may be empty and then
+  // stores zeros). Pair mode (two pieces): row
   // tiles L = n-1-j and S = j form pair j; slot j takes L whole or its first
   // piece, slot P+j takes S whole, slot 2P+odd+j L's second piece if L is
   // split (only where that beats L whole, counting kQPieceCost tiles for the
@@ -255,12 +259,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     n_tiles = qt == L ? nL : nS;
     full = qt == L ? fL : fS;
   } else {
-    piece = !middle && slot >= n_qtiles;
-    qt = middle ? P : n_qtiles - 1 - (piece ? slot - n_qtiles : slot);
+    piece = middle ? 0 : slot / n_qtiles;
+    qt = middle ? P : n_qtiles - 1 - slot % n_qtiles;
     tile_range(qt, 0, n_tiles, full);
     split = !middle && n_tiles > a.q_split;
-    t0 = split && piece ? (n_tiles + 1) / 2 : 0;
-    t1 = split && !piece ? (n_tiles + 1) / 2 : n_tiles;
+    const int h = (n_tiles + a.q_pieces - 1) / a.q_pieces;  // tiles per piece
+    t0 = split ? min(piece * h, n_tiles) : 0;
+    t1 = split ? min(t0 + h, n_tiles) : n_tiles;
     if (piece && !split) return;  // whole workgroup
   }
   const int row = qt * 32 * WAVES + wave * 32 + col;
@@ -477,7 +482,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
   if (split) {
     const int item = bh * n_qtiles + qt;
-    store_piece<NDT>(acc, a.q_part + (size_t)item * 2 * 4 * (NDT * 16 * 64), piece, a.q_count + item);
+    store_piece<NDT>(acc, a.q_part + (size_t)item * a.q_pieces * 4 * (NDT * 16 * 64), piece, a.q_count + item);
     return;
   }
   if (!row_in) return;
@@ -501,7 +506,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 // fragments stay in registers; dV^T += dO^T P and dK^T += Q^T dA take the
 // transposed operands from the staged tiles.
 template <typename T, int DP, int LOGB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void dense_bwd_dkv_fast_kernel(DenseArgs a, int n_rtiles, int n_ktiles) {
+// (head_dim 64: two workgroups per compute unit, so that one's prologue,
+// staging waits and epilogue overlap the other's products; at 128 the
+// registers allow one)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 2 : 1, DP == 64 ? 2 : 1))) void dense_bwd_dkv_fast_kernel(DenseArgs a, int n_rtiles, int n_ktiles) {
   typedef Mma<T> M;
   typedef typename M::Frag Frag;
   constexpr int WAVES = 4;
@@ -803,11 +811,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 }
 
 // ---------------------------------------------------------------------------
-// Sum of the two pieces of every split item: workgroup (w, t) with
+// Sum of the pieces of every split item (q_pieces for dQ, two for dK/dV):
+// workgroup (w, t) with
 // w < n_qitems handles accumulator tile t of dQ item w (128 rows), the rest
 // the dK/dV items (128 keys; tiles 0..NDT-1 dK, NDT.. dV). Thread (wave,
 // lane) holds the registers of the same (wave, lane) of the piece kernels,
 // i.e. row/key 32*wave + lane%32 and dims 32*dt + 8*(r/4) + 4*(lane/32) + r%4.
+// Sum over NP pieces of one accumulator tile's 16 registers of this lane
+// (every load issued before the additions).
+template <int NP>
+__device__ __forceinline__ void sum_pieces(const float* p0, size_t pstride, int t, float (&out)[16]) {
+  const int lane = threadIdx.x & 63;
+  float v[NP][16];
+#pragma unroll
+  for (int q = 0; q < NP; ++q)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) v[q][e] = p0[q * pstride + (t * 16 + e) * 64 + lane];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    float s = v[0][e];
+#pragma unroll
+    for (int q = 1; q < NP; ++q) s += v[q][e];
+    out[e] = s;
+  }
+}
+
 template <typename T, int DP>
 __global__ __launch_bounds__(256) void dense_bwd_merge_kernel(DenseArgs a, int n_qtiles, int n_ktiles) {
   constexpr int NDT = DP / 32;
@@ -825,8 +853,9 @@ __global__ __launch_bounds__(256) void dense_bwd_merge_kernel(DenseArgs a, int n
   const int64_t H = a.H, D = a.D;
   typedef T T4 __attribute__((ext_vector_type(4)));
   const int nacc = is_q ? NDT : 2 * NDT;
-  const float* p0 = (is_q ? a.q_part : a.k_part) + ((size_t)item * 2 * 4 + wave) * (nacc * 16 * 64);
-  const float* p1 = p0 + (size_t)4 * nacc * 16 * 64;
+  const int np = is_q ? a.q_pieces : 2;
+  const float* p0 = (is_q ? a.q_part : a.k_part) + ((size_t)item * np * 4 + wave) * (nacc * 16 * 64);
+  const size_t pstride = (size_t)4 * nacc * 16 * 64;
   if (idx >= (is_q ? a.Q : a.N)) return;
   // one accumulator tile per workgroup (blockIdx.y): dQ has NDT, dK/dV 2*NDT
   const int t = blockIdx.y;
@@ -837,14 +866,15 @@ __global__ __launch_bounds__(256) void dense_bwd_merge_kernel(DenseArgs a, int n
     T* dst;
     if (is_q) dst = reinterpret_cast<T*>(a.dq) + (((int64_t)bi * a.Q + idx) * H + hh) * D;
     else dst = reinterpret_cast<T*>(t < NDT ? a.dk : a.dv) + (((int64_t)bi * a.N + idx) * H + hh) * D;
+    float sum[16];
+    if (np == 8) sum_pieces<8>(p0, pstride, t, sum);
+    else if (np == 4) sum_pieces<4>(p0, pstride, t, sum);
+    else sum_pieces<2>(p0, pstride, t, sum);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       T4 o;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = (t * 16 + 4 * i + j) * 64 + lane;
-        o[j] = from_float<T>((p0[r] + p1[r]) * sc);
-      }
+      for (int j = 0; j < 4; ++j) o[j] = from_float<T>(sum[4 * i + j] * sc);
       *reinterpret_cast<T4*>(dst + 32 * dt + 8 * i + 4 * half) = o;
     }
   }
@@ -873,9 +903,15 @@ static hipError_t launch_fast(const DenseArgs& args, hipStream_t stream) {
   const unsigned BH = (unsigned)(a.B * a.H);
   // pair mode once slot mode's dQ slots outnumber the compute units
   a.q_pair = 2 * (int64_t)n_qtiles * BH > device_cus();
-  const int q_slots = a.q_pair ? 3 * (n_qtiles / 2) + (n_qtiles & 1) : 2 * n_qtiles;
-  a.k_pair = 2 * (int64_t)n_ktiles * BH > device_cus();
-  const int k_slots = a.k_pair ? 3 * (n_ktiles / 2) + (n_ktiles & 1) : 2 * n_ktiles;
+  if (a.q_pair) a.q_pieces = 2;
+  const int q_slots = a.q_pair ? 3 * (n_qtiles / 2) + (n_qtiles & 1) : a.q_pieces * n_qtiles;
+  // few query rows (at most kFewRTiles 64-row tiles): every visible key
+  // tile carries about the same work, so one workgroup per key tile, never
+  // split; else pair mode once slot mode's slots outnumber the compute units
+  const bool few_rows = n_rtiles <= kFewRTiles;
+  if (few_rows) a.k_split = n_rtiles;
+  a.k_pair = !few_rows && 2 * (int64_t)n_ktiles * BH > device_cus();
+  const int k_slots = a.k_pair ? 3 * (n_ktiles / 2) + (n_ktiles & 1) : (few_rows ? n_ktiles : 2 * n_ktiles);
   const int n_lim = (n_rows + 255) / 256;
   const int64_t pairs = (int64_t)a.B * a.Q * a.H;
   const int n_pre = (int)((pairs + 256 / (DP / 8) - 1) / (256 / (DP / 8)));

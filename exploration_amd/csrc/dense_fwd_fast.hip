@@ -73,11 +73,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int64_t H = a.H, D = a.D, N = a.N;
   constexpr int b = 1 << LOGB;
 
-  // The job of this workgroup: row tile qt, kind 0 (the tile whole or its
-  // first piece), 1 (its second piece; nothing if unsplit) or 2 (whole).
-  // Slot mode: 2 n_qtiles slots per head, slot k < n_qtiles takes kind 0 of
-  // row tile n_qtiles-1-k, slot n_qtiles+k kind 1 of it (longest causal rows
-  // first). Pair mode: row tiles L = n-1-j and S = j form pair j; slot j
+  // The job of this workgroup: row tile qt whole, or its piece `piece`.
+  // Slot mode: f_pieces n_qtiles slots per head, slot k takes piece
+  // k / n_qtiles of row tile n_qtiles-1-k % n_qtiles (longest causal rows
+  // first; the pieces of an unsplit tile other than the first do nothing).
+  // Pair mode: row tiles L = n-1-j and S = j form pair j; slot j
   // (j < n/2) takes L whole or its first piece, slot n/2+j takes S whole;
   // after an odd middle tile, slot 2(n/2)+odd+j takes L's second piece if L
   // is split, else nothing. L is split only where its second piece plus S,
@@ -140,9 +140,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     return t;
   };
 
-  int qt, kind;
+  int qt, piece = 0;
   bool split = false;  // this job is a piece of a split row tile
-  int hsplit = 0;      // remote tiles of a split tile's first piece
+  int hsplit = 0;      // remote tiles per piece (the last piece: the rest, and the local tiles)
   TileKeys tk;
   const bool middle = a.f_pair && (n_qtiles & 1) && slot == 2 * (n_qtiles / 2);
   if (a.f_pair && !middle) {
@@ -158,34 +158,37 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const bool sp = a.fw0 != nullptr && h > 0 && h < cL && max(h, cL - h + cS + kPieceCost) < cL;
     if (slot < P) {
       qt = L;  // L whole, or its first piece
-      kind = 0;
     } else if (slot < 2 * P) {
       qt = j;  // S whole
-      kind = 2;
     } else {
       if (!sp) return;  // L ran whole
       qt = L;  // L's second piece
-      kind = 1;
+      piece = 1;
     }
     split = sp && qt == L;
     hsplit = h;
     tk = qt == L ? tl : ts;
   } else {
+    // slot mode: slot k takes piece k / n_qtiles of row tile
+    // n_qtiles-1-k % n_qtiles (longest causal rows first); an odd middle
+    // tile of pair mode runs whole
     if (a.f_pair) {
-      qt = n_qtiles / 2;  // odd middle tile
-      kind = 2;
+      qt = n_qtiles / 2;
     } else {
-      kind = slot >= n_qtiles;
-      qt = n_qtiles - 1 - (kind ? slot - n_qtiles : slot);
+      piece = slot / n_qtiles;
+      qt = n_qtiles - 1 - slot % n_qtiles;
     }
     tk = tile_keys(row_keys(qt), 0);
     const int n_all = tk.n_remote_all + tk.n_local;
-    if (a.fw0 != nullptr && kind != 2 && n_all > a.f_split) {
+    if (a.fw0 != nullptr && !a.f_pair && n_all > a.f_split) {
       split = true;
-      hsplit = min((n_all + 1) / 2, tk.n_remote_all);
+      hsplit = (n_all + a.f_pieces - 1) / a.f_pieces;
     }
-    if (kind == 1 && !split) return;  // whole workgroup
+    if (piece > 0 && !split) return;  // whole workgroup
   }
+  // pieces of this job's row tile (pair mode: two)
+  const int n_pieces = split ? (a.f_pair ? 2 : a.f_pieces) : 1;
+  const bool last_piece = piece == n_pieces - 1;
   const int row = qt * 128 + wg * 32 + col;
   const bool row_in = row < a.Q;
   const RowKeys rk = row_keys(qt);
@@ -196,15 +199,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int full_remote = __builtin_amdgcn_readfirstlane(tk.full_remote);
   const int n_remote_all = __builtin_amdgcn_readfirstlane(tk.n_remote_all);
   const int lt0 = __builtin_amdgcn_readfirstlane(tk.lt0), n_local = __builtin_amdgcn_readfirstlane(tk.n_local);
-  // A split row tile runs as two pieces: piece 0 takes remote tiles [0, h),
-  // piece 1 remote tiles [h, n_remote_all) and the local tiles;
-  // dense_fwd_merge combines their partial results.
+  // A split row tile runs as n_pieces pieces: piece p takes remote tiles
+  // [p h, (p+1) h) (clipped to the remote range), the last piece the rest
+  // of them and the local tiles; dense_fwd_merge combines their partial
+  // results (a piece without tiles contributes nothing).
   if (!split) hsplit = n_remote_all;
-  const int piece = kind == 1;
   const int item = bh * n_qtiles + qt;
-  const int rs = __builtin_amdgcn_readfirstlane(piece ? hsplit : 0);               // first remote tile of this piece
-  const int n_remote = __builtin_amdgcn_readfirstlane(piece ? n_remote_all - hsplit : hsplit);  // remote tiles of this piece
-  const int n_loc = (!split || piece) ? n_local : 0;  // local tiles of this piece
+  const int rs = __builtin_amdgcn_readfirstlane(min(piece * hsplit, n_remote_all));  // first remote tile of this piece
+  const int re = last_piece ? n_remote_all : min((piece + 1) * hsplit, n_remote_all);
+  const int n_remote = __builtin_amdgcn_readfirstlane(re - rs);  // remote tiles of this piece
+  const int n_loc = last_piece ? n_local : 0;  // local tiles of this piece
   // this group's tiles: group 0 the first r0 remote tiles, then the local
   // ones; group 1 the other remote tiles (r0 balances the two counts)
   const int r0 = __builtin_amdgcn_readfirstlane(min(n_remote, max(0, (n_remote - n_loc + 1) / 2)));
@@ -275,7 +279,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // Group 0's end of the remote pass: join the halves of its sums and, when
   // local tiles follow, park its remote mean acc/dr in rc (one burst of
   // stores that drains while the local tiles run).
-  const bool park_rc = !(split && piece == 0);  // piece 0 keeps its remote sums for the epilogue
+  const bool park_rc = last_piece;  // other pieces keep their remote sums for the epilogue
   auto finish_remote = [&]() __attribute__((always_inline)) {
     zs_r += swap_halves(zs_r);
     dr += swap_halves(dr);
@@ -545,22 +549,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   if (a.fw0 != nullptr && !piece && threadIdx.x == 0) a.fflag[item] = split ? 1 : 0;
   float xa0, xa1;  // per row: weights of the two remote means in the written remote part
   float sf;        // scale of the staged acc
-  float* st8 = a.fstat + ((size_t)item * 128 + lrow) * 8;
-  if (split && piece == 0) {
-    // partial of piece 0: the joined remote mean
+  // this row's partial statistics: (max, row sum, sum of squared block
+  // sums) of piece p at 4 p, the local (max, row sum) at 4 n_pieces
+  float* st4 = a.fstat + ((size_t)item * 128 + lrow) * 4 * (n_pieces + 1);
+  if (split && !last_piece) {
+    // partial of a piece without local tiles: the joined remote mean
     xa0 = 0.f;
     xa1 = a1;
     sf = dr > 0.f ? a0 / dr : 0.f;  // acc holds group 0's unnormalised remote sums
     if (half == 0 && row_in) {
-      st8[0] = mx; st8[1] = zs; st8[2] = drs;
+      st4[4 * piece] = mx; st4[4 * piece + 1] = zs; st4[4 * piece + 2] = drs;
     }
   } else if (split) {
-    // partial of piece 1: the joined remote mean (rc) and the local mean
+    // partial of the last piece: the joined remote mean (rc) and the local mean
     xa0 = a0;
     xa1 = a1;
     sf = zsum > 0.f ? 1.f / zsum : 0.f;
     if (half == 0 && row_in) {
-      st8[3] = mx; st8[4] = zs; st8[5] = drs; st8[6] = m_l; st8[7] = zsum;
+      st4[4 * piece] = mx; st4[4 * piece + 1] = zs; st4[4 * piece + 2] = drs;
+      st4[4 * n_pieces] = m_l; st4[4 * n_pieces + 1] = zsum;
     }
   } else {
     const float dl = p >= 0 ? zsum : 0.f;
@@ -593,8 +600,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __threadfence_block();
   __builtin_amdgcn_wave_barrier();
   typedef T T4 __attribute__((ext_vector_type(4)));
-  const int mode = split ? (piece ? 1 : 0) : 2;
-  float* fdst = split ? (piece == 0 ? a.fw0 : a.fw1) + (size_t)item * 128 * D : nullptr;
+  const int mode = split ? (last_piece ? 1 : 0) : 2;
+  const size_t n_items = (size_t)BH * n_qtiles;
+  float* fdst = split ? (last_piece ? a.fw1 + (size_t)item * 128 * D
+                                    : a.fw0 + ((size_t)piece * n_items + item) * 128 * D)
+                      : nullptr;
   // every global load before the first store (the stores may alias in the
   // compiler's view, which would serialise the round trips)
   f32x4 mean[NIT];
@@ -628,13 +638,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 }
 
-// Combination of the two pieces of every split row tile: remote partials
-// (max m, row sum zs, sum of squared block sums dr, all at scale 2^-m, and
-// the remote means) merged at the common max, then the gate with the local
-// partial of piece 1 as in the single-piece epilogue. DP/8 threads per row,
-// 8 values each: every access is row-contiguous, and all loads of a thread
-// are issued before its arithmetic.
-template <typename T, int DP>
+// Combination of the pieces of every split row tile: the remote partials
+// (per piece: max m, row sum zs, sum of squared block sums dr, all at scale
+// 2^-m, and the remote mean) merged at the common max, then the gate with
+// the local partial of the last piece as in the single-piece epilogue. DP/8
+// threads per row, 8 values each: every access is row-contiguous, and all
+// loads of a thread are issued before its arithmetic.
+template <typename T, int DP, int P>
 __global__ __launch_bounds__(256) void dense_fwd_merge_kernel(DenseArgs a, int n_qtiles) {
   constexpr int TR = DP / 8;      // threads per row
   constexpr int RPW = 256 / TR;   // rows per workgroup
@@ -649,47 +659,51 @@ __global__ __launch_bounds__(256) void dense_fwd_merge_kernel(DenseArgs a, int n
   const int64_t H = a.H, D = a.D;
   const int64_t g = (((int64_t)bi * a.Q + row) * H + hh) * D + c;
   const size_t w = ((size_t)item * 128 + lrow) * D + c;
-  const float* st8 = a.fstat + ((size_t)item * 128 + lrow) * 8;
-  const f32x4 sa = *reinterpret_cast<const f32x4*>(st8), sb = *reinterpret_cast<const f32x4*>(st8 + 4);
+  const size_t piece_stride = (size_t)a.B * a.H * n_qtiles * 128 * D;
+  const float* st4 = a.fstat + ((size_t)item * 128 + lrow) * 4 * (P + 1);
   const int64_t p = a.pos[(int64_t)bi * a.Q + row];
-  f32x4 mean0[2], mean1[2], meanl[2];
+  f32x4 stat[P + 1], mean[P][2], meanl[2];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    mean0[h] = *reinterpret_cast<const f32x4*>(a.fw0 + w + 4 * h);
-    mean1[h] = *reinterpret_cast<const f32x4*>(a.rc + g + 4 * h);
-    meanl[h] = *reinterpret_cast<const f32x4*>(a.fw1 + w + 4 * h);
+  for (int i = 0; i <= P; ++i) stat[i] = *reinterpret_cast<const f32x4*>(st4 + 4 * i);
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const float* src = i < P - 1 ? a.fw0 + i * piece_stride + w : a.rc + g;
+    mean[i][0] = *reinterpret_cast<const f32x4*>(src);
+    mean[i][1] = *reinterpret_cast<const f32x4*>(src + 4);
   }
-  const float m0 = sa[0], zs0 = sa[1], dr0 = sa[2];
-  const float m1 = sa[3], zs1 = sb[0], dr1 = sb[1], ml = sb[2], zl = sb[3];
-  const float mx = fmaxf(m0, m1);
-  float zs = 0.f, w0 = 0.f, w1 = 0.f;
-  if (mx != kNegInf) {
-    const float e0 = fast_exp2(m0 - mx), e1 = fast_exp2(m1 - mx);
-    zs = zs0 * e0 + zs1 * e1;
-    w0 = dr0 * e0 * e0;
-    w1 = dr1 * e1 * e1;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) meanl[h] = *reinterpret_cast<const f32x4*>(a.fw1 + w + 4 * h);
+  float mx = kNegInf;
+#pragma unroll
+  for (int i = 0; i < P; ++i) mx = fmaxf(mx, stat[i][0]);
+  float zs = 0.f, drs = 0.f, wt[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const float e = mx != kNegInf ? fast_exp2(stat[i][0] - mx) : 0.f;
+    zs += stat[i][1] * e;
+    wt[i] = stat[i][2] * e * e;
+    drs += wt[i];
   }
-  const float drs = w0 + w1;
+  const float m_loc = stat[P][0], zl = stat[P][1];
   float log_zr = zs > 0.f ? log_mass(mx, zs) : kNegInf;
   float lr = drs > 0.f ? log_mass(mx, drs) - fast_log2(zs) * kLn2 : kNegInf;
-  float ll = zl > 0.f ? log_mass(ml, zl) : kNegInf;
+  float ll = zl > 0.f ? log_mass(m_loc, zl) : kNegInf;
   if (p < 0) { lr = kNegInf; ll = kNegInf; log_zr = kNegInf; }
   const float tot = logaddexp(lr, ll);
   const float safe_total = tot == kNegInf ? 0.f : tot;
   const float prem = lr == kNegInf ? 0.f : __expf(lr - safe_total);
   const float ploc = ll == kNegInf ? 0.f : __expf(ll - safe_total);
-  const float a0 = drs > 0.f ? prem * (w0 / drs) : 0.f, a1 = drs > 0.f ? prem * (w1 / drs) : 0.f;
+  const float f = drs > 0.f ? prem / drs : 0.f;
   typedef T T8 __attribute__((ext_vector_type(8)));
   T8 o;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    f32x4 rc;
+    f32x4 rc = {};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      rc[j] = a0 * mean0[h][j] + a1 * mean1[h][j];
-      o[4 * h + j] = from_float<T>(rc[j] + ploc * meanl[h][j]);
-    }
+    for (int i = 0; i < P; ++i) rc += mean[i][h] * (wt[i] * f);
     *reinterpret_cast<f32x4*>(a.rc + g + 4 * h) = rc;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[4 * h + j] = from_float<T>(rc[j] + ploc * meanl[h][j]);
   }
   *reinterpret_cast<T8*>(reinterpret_cast<T*>(a.out) + g) = o;
   if (c == 0) {
@@ -718,9 +732,12 @@ static hipError_t launch_fast(const DenseArgs& args, hipStream_t stream) {
   DenseArgs a = args;
   const int n_qtiles = (a.Q + 127) / 128;
   const unsigned items = (unsigned)(n_qtiles * a.B * a.H);
-  // pair mode once slot mode's slots outnumber the compute units
+  // pair mode (two pieces) once slot mode's two-piece slots outnumber the
+  // compute units; else slot mode with the workspace's piece count (more
+  // than two for launches with few row tiles)
   a.f_pair = a.fw0 != nullptr && 2 * (int64_t)items > device_cus();
-  const int per_head = a.f_pair ? 3 * (n_qtiles / 2) + (n_qtiles & 1) : a.fw0 != nullptr ? 2 * n_qtiles : n_qtiles;
+  if (a.f_pair) a.f_pieces = 2;
+  const int per_head = a.f_pair ? 3 * (n_qtiles / 2) + (n_qtiles & 1) : a.fw0 != nullptr ? a.f_pieces * n_qtiles : n_qtiles;
   dim3 grid((unsigned)(per_head * a.B * a.H));
   auto go = [&]<int LOGB>() {
     note_launch((const void*)&dense_fwd_fast_kernel<T, DP, LOGB>,
@@ -740,9 +757,14 @@ static hipError_t launch_fast(const DenseArgs& args, hipStream_t stream) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.fw0 == nullptr) return e;
   constexpr int WPI = 128 / (256 / (DP / 8));
-  note_launch((const void*)&dense_fwd_merge_kernel<T, DP>,
-              {"dense_fwd_merge", dtype_code<T>(), DP, a.block, 256 / (DP / 8), DP, 4, 0, items * WPI, "rows"});
-  hipLaunchKernelGGL((dense_fwd_merge_kernel<T, DP>), dim3(items * WPI), dim3(256), 0, stream, a, n_qtiles);
+  auto merge = [&]<int P>() {
+    note_launch((const void*)&dense_fwd_merge_kernel<T, DP, P>,
+                {"dense_fwd_merge", dtype_code<T>(), DP, a.block, 256 / (DP / 8), DP, 4, 0, items * WPI, "rows"});
+    hipLaunchKernelGGL((dense_fwd_merge_kernel<T, DP, P>), dim3(items * WPI), dim3(256), 0, stream, a, n_qtiles);
+  };
+  if (a.f_pieces == 8) merge.template operator()<8>();
+  else if (a.f_pieces == 4) merge.template operator()<4>();
+  else merge.template operator()<2>();
   return hipGetLastError();
 }
 
@@ -758,10 +780,11 @@ DenseFwdPlan dense_fwd_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t 
   const int64_t n_ktiles = (N + 127) / 128;
   if (n_ktiles < 4) return p;  // no row tile long enough to split: no workspace
   const size_t items = (size_t)(B * H) * p.n_qtiles;
+  p.pieces = split_pieces((int64_t)items);
   const size_t w = align256(items * 128 * (size_t)D * sizeof(float));
-  p.off_w1 = w;
-  p.off_stat = 2 * w;
-  p.off_flag = p.off_stat + align256(items * 128 * 8 * sizeof(float));
+  p.off_w1 = (p.pieces - 1) * w;
+  p.off_stat = p.pieces * w;
+  p.off_flag = p.off_stat + align256(items * 128 * 4 * (p.pieces + 1) * sizeof(float));
   p.total = p.off_flag + align256(items * sizeof(int));
   return p;
 }

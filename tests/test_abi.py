@@ -74,9 +74,10 @@ def test_argument_errors_map_to_value_error():
     # statistics and the (beta, eps) table (B*H*Qp*nblk*8 bytes)
     assert lib.st_dense_bwd_workspace_bytes(0, 2, 5, 7, 3, 64, 4) == 2 * 256
     # delta+rho 2*256, lim [2, 64] int32 512, tmin/tmax 2*256, table 2*3 heads x 32 blocks x 64 rows,
-    # two piece counters 2*256, dQ partials 6 items x 2 pieces x 128 x 64 floats, dK/dV twice that
+    # two piece counters 2*256, dQ partials 6 items x 8 pieces x 128 x 64 floats (six row tiles
+    # fill a small fraction of the chip: up to eight pieces each), dK/dV 6 items x 2 pieces x 2
     table = 2 * 3 * 32 * 64 * 8
-    partials = 6 * 2 * 128 * 64 * 4 * 3
+    partials = 6 * 128 * 64 * 4 * (8 + 2 * 2)
     assert lib.st_dense_bwd_workspace_bytes(2, 2, 5, 7, 3, 64, 4) == (2 * 256 + 512 + 2 * 256 + table + 2 * 256
                                                                        + partials)
     assert lib.st_dense_bwd_workspace_bytes(2, 2, 5, 7, 3, 64, 3) == 0
@@ -87,6 +88,16 @@ def test_argument_errors_map_to_value_error():
     inner = lib.st_dense_bwd_workspace_bytes(2, 2, 5, 7, 3, 64, 4)
     assert lib.st_dense_bwd_workspace_bytes(2, 2, 5, 7, 3, 60, 4) == (
         pad(inner) + 4 * pad(rq * 2) + 4 * pad(rk * 2) + pad(rq * 4))
+    # bf16 forward, the cfg5 read-chunk shape (240 queries over 8192 keys, H16 D64): 32 row
+    # tiles, so eight pieces per tile: seven remote means, the local mean, per row and piece
+    # four statistics plus four local ones, and the split flags
+    items, w = 32, 32 * 128 * 64 * 4
+    assert lib.st_dense_fwd_workspace_bytes(2, 1, 240, 8192, 16, 64, 16) == (
+        8 * w + 32 * 128 * 4 * 9 * 4 + pad(items * 4))
+    # cfg2 (256 row tiles): two pieces
+    w2 = 256 * 128 * 128 * 4
+    assert lib.st_dense_fwd_workspace_bytes(2, 1, 4096, 4096, 8, 128, 128) == (
+        2 * w2 + 256 * 128 * 4 * 3 * 4 + pad(256 * 4))
     # fp32 head_dim 17 (generic kernels, no workspace of their own) at 24:
     # q, k, v, out and rc copies
     assert lib.st_dense_fwd_workspace_bytes(0, 1, 3, 3, 1, 17, 4) == 5 * pad(3 * 24 * 4)

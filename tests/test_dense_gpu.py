@@ -157,6 +157,31 @@ def test_cfg5_shaped_chunk(device):
     _check_dense(q, k, v, pos, probe, b, device, torch.bfloat16, oracle_device=device, label="cfg5")
 
 
+@pytest.mark.parametrize("heads,rows,pieces", [(16, 240, 8), (32, 256, 4), (48, 256, 2)])
+def test_few_row_tiles_run_in_pieces(device, heads, rows, pieces):
+    """Launches with few 128-row tiles (B*H*tiles well below the compute
+    units: the cfg5 read chunks) run every row tile's key range as up to
+    eight pieces, forward and dQ, whose partials merge kernels combine:
+    consecutive positions near the end of N=8192 keys (D64 b16, bf16), with
+    a padding row and a row at key 0. The launch record shows the piece
+    count (workgroups = pieces x row tiles x heads); oracle in float32 on
+    the GPU."""
+    print(f"dense pieces heads={heads} rows={rows}", flush=True)
+    g = torch.Generator().manual_seed(30 + heads)
+    n, d, b = 8192, 64, 16
+    q = (torch.randn(1, rows, heads, d, generator=g) / 8).to(torch.bfloat16)
+    k = (torch.randn(1, n, heads, d, generator=g) / 8).to(torch.bfloat16)
+    v = torch.randn(1, n, heads, d, generator=g).to(torch.bfloat16)
+    probe = torch.randn(1, rows, heads, d, generator=g).to(torch.bfloat16)
+    pos = torch.arange(n - 100 - rows, n - 100)[None].clone()
+    pos[0, 0], pos[0, 1] = -1, 0
+    _check_dense(q, k, v, pos, probe, b, device, torch.bfloat16, oracle_device=device, label=f"pieces{pieces}")
+    tiles = -(-rows // 128)
+    fwd = [r for r in launch_report() if r.get("kernel") == "dense_fwd_fast" and r.get("head_dim") == 64
+           and r.get("block_size") == 16 and r.get("mode") == "slot"]
+    assert fwd and fwd[-1]["workgroups"] == pieces * tiles * heads, fwd
+
+
 def test_cfg2_full_size(device):
     """cfg2 at full size: bf16 B1 H8 N=Q=4096 D128 b128, causal; q/k/v ~
     N(0,1)/sqrt(128), dO ~ N(0,1) (oracle in float32 on the GPU)."""
