@@ -334,18 +334,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     };
     // S^T products contraction chunk outermost (product j: chunk j / NST,
     // subtile j % NST), so each Q fragment is read once per phase
+    // (the Q fragment of contraction chunk c is read with chunk c's K
+    // fragments, one chunk ahead)
     auto s_load = [&](int j) __attribute__((always_inline)) { return kfrag(j % NST, j / NST); };
-    Frag qc;
-    auto s_mma = [&](int j, Frag f) __attribute__((always_inline)) {
+    auto s_mma = [&](int j, Frag f, Frag qc) __attribute__((always_inline)) {
       const int st = j % NST, c = j / NST;
-      if (st == 0) qc = *reinterpret_cast<const Frag*>(lds + qoff + 2048 * c);
       sc[st] = M::mma(f, qc, c == 0 ? zero16() : sc[st]);
     };
-    mfma_chunks<NPV + NSP, 4, NPV>(
+    static_assert(NST == 4, "one contraction chunk per MFMA chunk");
+    mfma_chunks_shared<NPV + NSP, 4, NPV, NPV>(
         [&](int j) __attribute__((always_inline)) { return j < NPV ? pv_load(j) : s_load(j - NPV); },
-        [&](int j, Frag f) __attribute__((always_inline)) {
+        [&](int g) __attribute__((always_inline)) {
+          return *reinterpret_cast<const Frag*>(lds + qoff + 2048 * (g - NPV / 4));
+        },
+        [&](int j, Frag f, Frag qc) __attribute__((always_inline)) {
           if (j < NPV) pv_mma(j, f);
-          else s_mma(j - NPV, f);
+          else s_mma(j - NPV, f, qc);
         });
     // group 0: the last remote PV products (tile my_remote - 1) are in
     if (grp == 0 && k == my_remote) finish_remote();

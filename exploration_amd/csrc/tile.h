@@ -546,6 +546,43 @@ __device__ __forceinline__ void mfma_chunks(Load&& load, Mfma&& mma) {
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// mfma_chunks where the chunks from NQ0 on also read one fragment shared by
+// their L products (the B operand of the S^T products, one Q fragment per
+// contraction chunk): it is read with the chunk's own operands, one chunk
+// ahead, and handed to mma(j, f, shared) (chunks before NQ0 get an unused
+// fragment).
+template <int N, int L, int NR2, int NQ0, typename Load, typename QLoad, typename Mfma>
+__device__ __forceinline__ void mfma_chunks_shared(Load&& load, QLoad&& qload, Mfma&& mma) {
+  static_assert(N % L == 0 && NR2 % L == 0 && NQ0 % L == 0, "phase must split into whole chunks");
+  constexpr int C = N / L;
+  typedef decltype(load(0)) F;
+  F buf[2][L];
+  F qb[2];
+#pragma unroll
+  for (int i = 0; i < L; ++i) buf[0][i] = load(i);
+  if constexpr (NQ0 == 0) qb[0] = qload(0);
+  [&]<int... G>(std::integer_sequence<int, G...>) {
+    ([&] {
+      constexpr int g = G;
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt untouched
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (g + 1 < C) {
+#pragma unroll
+        for (int i = 0; i < L; ++i) buf[(g + 1) & 1][i] = load((g + 1) * L + i);
+        if constexpr ((g + 1) * L >= NQ0) qb[(g + 1) & 1] = qload(g + 1);
+      }
+#pragma unroll
+      for (int i = 0; i < L; ++i) mma(g * L + i, buf[g & 1][i], qb[g & 1]);
+      if constexpr (g + 1 < C)
+        __builtin_amdgcn_sched_group_barrier(
+            0x100, L * ((g + 1) * L < NR2 ? 2 : 1) + ((g + 1) * L >= NQ0 ? 1 : 0), 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, L, 0);
+    }(), ...);
+  }(std::make_integer_sequence<int, C>{});
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // Half-wave exchange: returns x of the lane 32 positions away.
 __device__ __forceinline__ float swap_halves(float x) { return other_half(x); }
 
