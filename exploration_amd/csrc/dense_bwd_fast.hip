@@ -595,6 +595,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 
   const int kb = kt_idx * kKT;
   const int key = kb + 32 * wave + col;
 
+  // No row reaches these keys (every row tile's last visible key is below
+  // kb): dK = dV = 0. Each wave decides by itself (one load per lane and
+  // 64 row tiles) and writes its 32 zero rows with 16-byte stores, before
+  // any K/V load.
+  {
+    bool any = false;
+    for (int c0 = 0; c0 < n_rtiles && !any; c0 += 64) {
+      const int t = c0 + lane;
+      any = __ballot(t < n_rtiles && tmax[t] >= kb) != 0;
+    }
+    if (!any) {
+      if (piece) return;  // the tile's first slot writes the zeros
+      constexpr int LPR = DP * (int)sizeof(T) / 16;  // lanes per key row
+      constexpr int RPI = 64 / LPR;                   // rows per store instruction
+      typedef typename Vec16<T>::type V;
+#pragma unroll
+      for (int it = 0; it < 32 / RPI; ++it) {
+        const int k = kb + 32 * wave + it * RPI + lane / LPR;
+        if (k < a.N) {
+          const int64_t off = (((int64_t)bi * N + k) * H + hh) * D + (lane % LPR) * Vec16<T>::n;
+          *reinterpret_cast<V*>(reinterpret_cast<T*>(a.dk) + off) = V{};
+          *reinterpret_cast<V*>(reinterpret_cast<T*>(a.dv) + off) = V{};
+        }
+      }
+      return;
+    }
+  }
+
   // row tiles that see a key of this workgroup, in order; bit 0 marks tiles
   // whose rows all see every key of it (no masks)
   if (wave == 0) {

@@ -209,6 +209,23 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int re = last_piece ? n_remote_all : min((piece + 1) * hsplit, n_remote_all);
   const int n_remote = __builtin_amdgcn_readfirstlane(re - rs);  // remote tiles of this piece
   const int n_loc = last_piece ? n_local : 0;  // local tiles of this piece
+  if (split && n_remote == 0 && n_loc == 0) {
+    // a piece without tiles (only a non-last piece can be one): its
+    // statistics say "no mass", its mean is zero, and the first piece marks
+    // the item as split
+    const int lrow = wg * 32 + col;
+    float* mean0 = a.fw0 + ((size_t)piece * BH * n_qtiles + bh * n_qtiles + qt) * 128 * D;
+    for (int i = threadIdx.x; i < 128 * DP / 4; i += 512)
+      if (qt * 128 + (4 * i) / DP < a.Q) reinterpret_cast<f32x4*>(mean0)[i] = f32x4{};
+    if (grp == 0 && half == 0 && qt * 128 + lrow < a.Q) {
+      float* st4 = a.fstat + ((size_t)(bh * n_qtiles + qt) * 128 + lrow) * 4 * (n_pieces + 1) + 4 * piece;
+      st4[0] = kNegInf;
+      st4[1] = 0.f;
+      st4[2] = 0.f;
+    }
+    if (!piece && threadIdx.x == 0) a.fflag[bh * n_qtiles + qt] = 1;
+    return;
+  }
   // this group's tiles: group 0 the first r0 remote tiles, then the local
   // ones; group 1 the other remote tiles (r0 balances the two counts)
   const int r0 = __builtin_amdgcn_readfirstlane(min(n_remote, max(0, (n_remote - n_loc + 1) / 2)));
@@ -702,9 +719,11 @@ __global__ __launch_bounds__(256) void dense_fwd_merge_kernel(DenseArgs a, int n
   T8 o;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
+    // (a piece without mass has weight 0: selected away, not multiplied)
     f32x4 rc = {};
 #pragma unroll
-    for (int i = 0; i < P; ++i) rc += mean[i][h] * (wt[i] * f);
+    for (int i = 0; i < P; ++i)
+      if (wt[i] > 0.f) rc += mean[i][h] * (wt[i] * f);
     *reinterpret_cast<f32x4*>(a.rc + g + 4 * h) = rc;
 #pragma unroll
     for (int j = 0; j < 4; ++j) o[4 * h + j] = from_float<T>(rc[j] + ploc * meanl[h][j]);
