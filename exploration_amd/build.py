@@ -21,8 +21,16 @@ ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC",
-    # no packed fp32 instructions anywhere in the device code
+    # no packed fp32 instructions anywhere in the device code, and no
+    # mixed-precision VOP3P forms either (v_fma_mix*/v_mad_mix*: fp32 FMAs
+    # with fp16 operands or half-register fp16 results, which hipcc otherwise
+    # folds the fp16 conversions into). Both belong to the packed-math
+    # datapath whose results have not been reliable on this platform: dQ
+    # fragments assembled from v_fma_mix{lo,hi}_f16 writes came out wrong at
+    # fp16, head_dim 64, block 8, while the same kernel with separate FMA and
+    # conversion instructions is exact. bf16 code never uses them.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Xclang", "-target-feature", "-Xclang", "-fma-mix-insts",
     # no NaN inputs are meaningful here: without IEEE mode, v_max/v_min need
     # no canonicalising copy of each operand (one VALU op per max saved)
     "-fno-honor-nans", "-mno-amdgpu-ieee",

@@ -85,14 +85,9 @@ template <typename T> constexpr int dtype_code() {
   return sizeof(T) == 4 ? 0 : (__is_same(T, f16) ? 1 : 2);
 }
 
+// (the library is built without the mixed-precision v_fma_mix* forms, so an
+// fp16 result is a separate v_cvt_f16_f32 of a full fp32 value)
 template <typename T> __device__ __forceinline__ T from_float(float x) { return (T)x; }
-// fp32 -> fp16 keeps the value in a full VGPR first: otherwise hipcc folds
-// the fma/mul that produced it into v_fma_mix{lo,hi}_f16, and fragments built
-// from those half-register writes gave wrong dQ tiles on gfx950.
-template <> __device__ __forceinline__ f16 from_float<f16>(float x) {
-  __asm__("" : "+v"(x));
-  return (f16)x;
-}
 template <typename T> __device__ __forceinline__ float to_float(T x) { return (float)x; }
 
 __device__ __forceinline__ f32x16 zero16() {
