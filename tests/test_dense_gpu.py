@@ -182,6 +182,26 @@ def test_few_row_tiles_run_in_pieces(device, heads, rows, pieces):
     assert fwd and fwd[-1]["workgroups"] == pieces * tiles * heads, fwd
 
 
+@pytest.mark.parametrize("d,b,dtype", [(128, 32, torch.float16), (64, 128, torch.bfloat16), (64, 2, torch.bfloat16)],
+                         ids=str)
+def test_few_row_pieces_ragged(device, d, b, dtype):
+    """The eight-piece path (6 row tiles for 256 compute units) with batch 2,
+    3 heads, 130 query rows (a partial second row tile) at unsorted positions
+    over 3,000 keys: padding rows, rows at key 0, rows past the last key, and
+    pieces left without key tiles (oracle in float32 on the GPU)."""
+    print(f"dense ragged pieces d={d} b={b} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(40 + d + b)
+    n, rows = 3000, 130
+    q = (torch.randn(2, rows, 3, d, generator=g) / math.sqrt(d)).to(dtype)
+    k = (torch.randn(2, n, 3, d, generator=g) / math.sqrt(d)).to(dtype)
+    v = torch.randn(2, n, 3, d, generator=g).to(dtype)
+    probe = torch.randn(2, rows, 3, d, generator=g).to(dtype)
+    pos = torch.randint(-1, n + 50, (2, rows), generator=g)
+    pos[0, :5] = torch.tensor([0, -1, n - 1, n + 7, 1])
+    pos[1, -3:] = torch.tensor([b, 2 * b - 1, 130])
+    _check_dense(q, k, v, pos, probe, b, device, dtype, oracle_device=device, label=f"ragged d={d} b={b}")
+
+
 def test_cfg2_full_size(device):
     """cfg2 at full size: bf16 B1 H8 N=Q=4096 D128 b128, causal; q/k/v ~
     N(0,1)/sqrt(128), dO ~ N(0,1) (oracle in float32 on the GPU)."""
