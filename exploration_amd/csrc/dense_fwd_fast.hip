@@ -331,6 +331,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   float gate[NST];
 #pragma unroll
   for (int st = 0; st < NST; ++st) gate[st] = 1.f;
+  // the probabilities of the group's last tile as 16-bit PV operands
+  // (subtile st, 16-key half c2), made at the end of its softmax phase:
+  // with two waves per SIMD the other group's softmax keeps the vector unit
+  // busy during an MFMA phase, so the conversions belong to the softmax
+  // phase (phase 0 multiplies zeros)
+  Frag pb[NST][2];
+#pragma unroll
+  for (int st = 0; st < NST; ++st) pb[st][0] = pb[st][1] = Frag{};
 
   // MFMA phase k: PV products of the group's tile k-1 (V in vbuf) first,
   // then the S^T products of its tile k (K in kbuf), in chunks of 4 with the
@@ -344,10 +352,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     auto pv_load = [&](int q) __attribute__((always_inline)) { return vfrag(16 * (q / NDT), q % NDT); };
     auto pv_mma = [&](int q, Frag f) __attribute__((always_inline)) {
       const int st = q / (2 * NDT), c2 = (q / NDT) & 1;
-      Frag b;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) b[e] = from_float<T>(sc[st][8 * c2 + e] * gate[st]);
-      acc[q % NDT] = M::mma(f, b, acc[q % NDT]);
+      acc[q % NDT] = M::mma(f, pb[st][c2], acc[q % NDT]);
     };
     // S^T products contraction chunk outermost (product j: chunk j / NST,
     // subtile j % NST), so each Q fragment is read once per phase
@@ -467,6 +472,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) acc[dt] *= f;
     }
+#pragma unroll
+    for (int st = 0; st < NST; ++st)
+#pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pb[st][c2][e] = from_float<T>(sc[st][8 * c2 + e] * gate[st]);
   };
 
   // Phases: MFMA(0), softmax(0), MFMA(1), ..., softmax(n-1), MFMA(n) for the
