@@ -33,7 +33,7 @@ struct DenseArgs {
   // adds afterwards (flags zeroed by the rows kernel)
   int* q_count;           // [B*H*n_qtiles] 1 if the dQ item was split
   int* k_count;           // [B*H*n_ktiles] 1 if the dK/dV item was split
-  float* q_part;          // dQ partials, [item][piece][wave][register][lane]
+  float* q_part;          // dQ partials, [item][piece][wave][tile][register quad][lane] x 4
   float* k_part;          // dK/dV partials, same order
   int q_split, k_split;   // items with more tiles than this run in pieces
   int q_pieces;           // pieces of a split dQ item (2, or up to kMaxPieces for few items)

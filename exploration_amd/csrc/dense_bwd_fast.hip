@@ -151,18 +151,19 @@ __global__ __launch_bounds__(256) void dense_bwd_prep_kernel(DenseArgs a, int n_
   }
 }
 
-// A piece of a split item stores its fp32 accumulators in register order
-// ([piece][wave][register][lane], so a wave's stores are lane-contiguous);
-// dense_bwd_merge adds the two pieces after the kernel. The first piece
-// marks the item as split.
+// A piece of a split item stores its fp32 accumulators in register-quad
+// order ([piece][wave][tile][quad][lane] x 4 floats: one 16-byte store per
+// lane and quad, a wave's 1 KiB contiguous); dense_bwd_merge adds the
+// pieces after the kernel. The first piece marks the item as split.
 template <int NACC>
 __device__ __forceinline__ void store_piece(const f32x16 (&acc)[NACC], float* part, int piece, int* flag) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  float* mine = part + ((size_t)piece * 4 + wave) * (NACC * 16 * 64);
+  f32x4* mine = reinterpret_cast<f32x4*>(part + ((size_t)piece * 4 + wave) * (NACC * 16 * 64));
 #pragma unroll
   for (int t = 0; t < NACC; ++t)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) mine[(t * 16 + r) * 64 + lane] = acc[t][r];
+    for (int q = 0; q < 4; ++q)
+      mine[(t * 4 + q) * 64 + lane] = f32x4{acc[t][4 * q], acc[t][4 * q + 1], acc[t][4 * q + 2], acc[t][4 * q + 3]};
   if (piece == 0 && threadIdx.x == 0) *flag = 1;
 }
 
@@ -850,16 +851,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 
 template <int NP>
 __device__ __forceinline__ void sum_pieces(const float* p0, size_t pstride, int t, float (&out)[16]) {
   const int lane = threadIdx.x & 63;
-  float v[NP][16];
+  f32x4 v[NP][4];
 #pragma unroll
   for (int q = 0; q < NP; ++q)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) v[q][e] = p0[q * pstride + (t * 16 + e) * 64 + lane];
+    for (int i = 0; i < 4; ++i) v[q][i] = reinterpret_cast<const f32x4*>(p0 + q * pstride)[(t * 4 + i) * 64 + lane];
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
-    float s = v[0][e];
+    float s = v[0][e >> 2][e & 3];
 #pragma unroll
-    for (int q = 1; q < NP; ++q) s += v[q][e];
+    for (int q = 1; q < NP; ++q) s += v[q][e >> 2][e & 3];
     out[e] = s;
   }
 }
