@@ -351,7 +351,7 @@ def main():
                    "global_batch": 1, "seq_len": 4096, "heads": 8, "head_dim": 128, "block_size": 128,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": "dense forward+backward, one step (dense_fwd_fast, "
-                     "dense_fwd_merge, dense_bwd_prep, dense_bwd_dq_fast, dense_bwd_dkv_fast, dense_bwd_merge)",
+                     "dense_fwd_merge, dense_bwd_dq_fast, dense_bwd_dkv_fast, dense_bwd_merge)",
                      "achieved": round(dense["tflops"], 3), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(dense["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic[0],
                      "traffic_unit": "bytes per step (calibrated FETCH_SIZE + WRITE_SIZE)",

@@ -18,11 +18,11 @@
 //   beyond the row's window: beta_j = +inf (P = 0), eps_j = 0.
 //
 // Kernels:
-//  * dense_bwd_prep: delta and rho per row; per row the last visible key,
-//    per 64-row tile its min/max (which row tiles a key tile must visit,
-//    and which need masks);
 //  * dense_bwd_dq_fast: lane = query row, the layout in which block sums are
-//    in-lane; recomputes S and dP, writes dQ and the (beta, eps) table;
+//    in-lane; computes delta and rho of its rows (st/ops/kernels/dense.py:
+//    89-100), recomputes S and dP, writes dQ and the (beta, eps) table, and
+//    per row the last visible key, per 64-row tile its min/max (which row
+//    tiles a key tile must visit, and which need masks);
 //  * dense_bwd_dkv_fast: lane = key; per element one exp2 and two FMAs from
 //    the table, no cross-lane or cross-wave reductions, dK/dV in registers.
 // K/V (dQ kernel) and Q/dO (dK/dV kernel) tiles are staged with asynchronous
@@ -91,72 +91,13 @@ DenseBwdPlan dense_bwd_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t 
   return p;
 }
 
-// ---------------------------------------------------------------------------
-// Preparation, one launch with two kinds of workgroup:
-//  * the first n_lim workgroups: per row the last visible key (min(p, N-1);
-//    -1 for padding rows and rows beyond Q), per 64-row tile (one wave) its
-//    min and max, and the split flags of both kernels cleared;
-//  * the rest: delta = dO.O and rho = dO.RC - delta*PR per (row, head),
-//    DP/8 threads per (row, head) with 16-byte loads of dO and O and two of
-//    RC (st/ops/kernels/dense.py:89-100).
-template <typename T, int DP>
-__global__ __launch_bounds__(256) void dense_bwd_prep_kernel(DenseArgs a, int n_lim, int n_qitems, int n_kitems) {
-  if ((int)blockIdx.x < n_lim) {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    for (int64_t i = idx; i < n_qitems; i += (int64_t)n_lim * 256) a.q_count[i] = 0;
-    for (int64_t i = idx; i < n_kitems; i += (int64_t)n_lim * 256) a.k_count[i] = 0;
-    // B*Qp is a multiple of 64: whole waves leave together
-    if (idx >= (int64_t)a.B * a.Qp) return;
-    const int bi = (int)(idx / a.Qp), row = (int)(idx % a.Qp);
-    int lim = -1;
-    if (row < a.Q) {
-      const int64_t p = a.pos[(int64_t)bi * a.Q + row];
-      if (p >= 0) lim = (int)(p < a.N - 1 ? p : a.N - 1);
-    }
-    a.lim[idx] = lim;
-    const int mx = wave_max(lim), mn = wave_min(lim);
-    if ((threadIdx.x & 63) == 0) {
-      a.tmax[idx / kRT] = mx;
-      a.tmin[idx / kRT] = mn;
-    }
-    return;
-  }
-  constexpr int TR = DP / 8;  // threads per (row, head)
-  const int64_t pair = ((int64_t)blockIdx.x - n_lim) * (256 / TR) + threadIdx.x / TR;
-  const bool in = pair < (int64_t)a.B * a.Q * a.H;
-  const int c = (threadIdx.x % TR) * 8;
-  typedef T T8 __attribute__((ext_vector_type(8)));
-  float dsum = 0.f, rsum = 0.f;
-  if (in) {
-    const int64_t e = pair * DP + c;
-    const T8 g = *reinterpret_cast<const T8*>(reinterpret_cast<const T*>(a.dout) + e);
-    const T8 o = *reinterpret_cast<const T8*>(reinterpret_cast<const T*>(a.out) + e);
-    const f32x4 r0 = *reinterpret_cast<const f32x4*>(a.rc + e);
-    const f32x4 r1 = *reinterpret_cast<const f32x4*>(a.rc + e + 4);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float gv = to_float<T>(g[j]);
-      dsum += gv * to_float<T>(o[j]);
-      rsum += gv * (j < 4 ? r0[j] : r1[j - 4]);
-    }
-  }
-#pragma unroll
-  for (int off = TR / 2; off > 0; off >>= 1) {
-    dsum += __shfl_xor(dsum, off, 64);
-    rsum += __shfl_xor(rsum, off, 64);
-  }
-  if (in && c == 0) {
-    a.delta[pair] = dsum;
-    a.rho[pair] = rsum - dsum * a.pr[pair];
-  }
-}
-
 // A piece of a split item stores its fp32 accumulators in register-quad
 // order ([piece][wave][tile][quad][lane] x 4 floats: one 16-byte store per
 // lane and quad, a wave's 1 KiB contiguous); dense_bwd_merge adds the
-// pieces after the kernel. The first piece marks the item as split.
+// pieces after the kernel (the item's first piece records whether it was
+// split).
 template <int NACC>
-__device__ __forceinline__ void store_piece(const f32x16 (&acc)[NACC], float* part, int piece, int* flag) {
+__device__ __forceinline__ void store_piece(const f32x16 (&acc)[NACC], float* part, int piece) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   f32x4* mine = reinterpret_cast<f32x4*>(part + ((size_t)piece * 4 + wave) * (NACC * 16 * 64));
 #pragma unroll
@@ -164,7 +105,6 @@ __device__ __forceinline__ void store_piece(const f32x16 (&acc)[NACC], float* pa
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       mine[(t * 4 + q) * 64 + lane] = f32x4{acc[t][4 * q], acc[t][4 * q + 1], acc[t][4 * q + 2], acc[t][4 * q + 3]};
-  if (piece == 0 && threadIdx.x == 0) *flag = 1;
 }
 
 // ---------------------------------------------------------------------------
@@ -187,6 +127,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   __shared__ __attribute__((aligned(16))) T v0s[TILE];
   __shared__ __attribute__((aligned(16))) T v1s[TILE];
   __shared__ int range[2][2][WAVES];  // two row tiles: this one and the pair partner
+  __shared__ int lim_mm[2][WAVES];    // per wave: min and max of its rows' last visible keys
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 31, half = lane >> 5;
@@ -289,10 +230,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       base_r = zr * kLog2e;
       ezrz = __expf(zr - z);
     }
-    dl = a.delta[sidx];
-    rho = a.rho[sidx];
   }
   (void)n_tiles;
+  // The item's first piece: whether the item was split (for the merge), and
+  // per row the last visible key (min(p, N-1); -1 for padding rows and rows
+  // beyond Q), per 64-row tile its min and max (for the dK/dV kernel).
+  if (piece == 0) {
+    const int64_t item = (int64_t)bh * n_qtiles + qt;
+    if (threadIdx.x == 0) a.q_count[item] = split ? 1 : 0;
+    if (hh == 0) {
+      const int lim = p >= 0 ? (int)(p < N - 1 ? p : N - 1) : -1;
+      if (row < a.Qp && half == 0) a.lim[(int64_t)bi * a.Qp + row] = lim;
+      const int mx = wave_max(lim), mn = wave_min(lim);
+      if (lane == 0) { lim_mm[0][wave] = mn; lim_mm[1][wave] = mx; }
+      __syncthreads();
+      const int rt = row / kRT;  // the 64-row tile of waves 2w' and 2w'+1
+      if (lane == 0 && (wave & 1) == 0 && rt < a.Qp / kRT) {
+        a.tmin[(int64_t)bi * (a.Qp / kRT) + rt] = min(lim_mm[0][wave], lim_mm[0][wave + 1]);
+        a.tmax[(int64_t)bi * (a.Qp / kRT) + rt] = max(lim_mm[1][wave], lim_mm[1][wave + 1]);
+      }
+    }
+  }
 
   const T* kg = reinterpret_cast<const T*>(a.k) + ((int64_t)bi * N * H + hh) * D;
   const T* vg = reinterpret_cast<const T*>(a.v) + ((int64_t)bi * N * H + hh) * D;
@@ -313,6 +271,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     for (int c = 0; c < NKC; ++c) {
       qf[c] = row_in ? *reinterpret_cast<const Frag*>(qrow + c * 16 + half * 8) : Frag{};
       gf[c] = row_in ? *reinterpret_cast<const Frag*>(grow + c * 16 + half * 8) : Frag{};
+    }
+  }
+  // delta = dO.O and rho = dO.RC - delta*PR of this lane's row
+  // (st/ops/kernels/dense.py:89-100): this lane's half of the head dim, then
+  // the other half's from lane ^ 32
+  {
+    const T* orow = reinterpret_cast<const T*>(a.out) + obase;
+    const float* rrow = a.rc + obase;
+    float dsum = 0.f, rsum = 0.f;
+#pragma unroll
+    for (int c = 0; c < NKC; ++c) {
+      const Frag o = *reinterpret_cast<const Frag*>(orow + c * 16 + half * 8);
+      const f32x4 r0 = *reinterpret_cast<const f32x4*>(rrow + c * 16 + half * 8);
+      const f32x4 r1 = *reinterpret_cast<const f32x4*>(rrow + c * 16 + half * 8 + 4);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float g = to_float<T>(gf[c][e]);
+        dsum = fmaf(g, to_float<T>(o[e]), dsum);
+        rsum = fmaf(g, e < 4 ? r0[e] : r1[e - 4], rsum);
+      }
+    }
+    dsum += __shfl_xor(dsum, 32, 64);
+    rsum += __shfl_xor(rsum, 32, 64);
+    if (p >= 0) {
+      dl = dsum;
+      rho = rsum - dsum * a.pr[((int64_t)bi * a.Q + row) * H + hh];
     }
   }
 
@@ -483,7 +467,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
   if (split) {
     const int item = bh * n_qtiles + qt;
-    store_piece<NDT>(acc, a.q_part + (size_t)item * a.q_pieces * 4 * (NDT * 16 * 64), piece, a.q_count + item);
+    store_piece<NDT>(acc, a.q_part + (size_t)item * a.q_pieces * 4 * (NDT * 16 * 64), piece);
     return;
   }
   if (!row_in) return;
@@ -608,6 +592,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 
     }
     if (!any) {
       if (piece) return;  // the tile's first slot writes the zeros
+      if (threadIdx.x == 0) a.k_count[(int64_t)bh * n_ktiles + kt_idx] = 0;
       constexpr int LPR = DP * (int)sizeof(T) / 16;  // lanes per key row
       constexpr int RPI = 64 / LPR;                   // rows per store instruction
       typedef typename Vec16<T>::type V;
@@ -661,6 +646,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 
     hsplit = (n_act + 1) / 2;
     if (piece && !split) return;  // whole workgroup
   }
+  if (piece == 0 && threadIdx.x == 0) a.k_count[(int64_t)bh * n_ktiles + kt_idx] = split ? 1 : 0;
   const int i0 = split && piece ? hsplit : 0;
   const int i1 = split && !piece ? hsplit : n_act;
 
@@ -816,7 +802,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) { both[dt] = dk[dt]; both[NDT + dt] = dv[dt]; }
     const int item = bh * n_ktiles + kt_idx;
-    store_piece<2 * NDT>(both, a.k_part + (size_t)item * 2 * 4 * (2 * NDT * 16 * 64), piece, a.k_count + item);
+    store_piece<2 * NDT>(both, a.k_part + (size_t)item * 2 * 4 * (2 * NDT * 16 * 64), piece);
     return;
   }
   if (key >= a.N) return;
@@ -925,7 +911,6 @@ static int device_cus() {
 template <typename T, int DP>
 static hipError_t launch_fast(const DenseArgs& args, hipStream_t stream) {
   DenseArgs a = args;
-  const int n_rows = a.B * a.Qp;
   const int n_qtiles = (a.Q + 127) / 128;
   const int n_ktiles = (a.N + kKT - 1) / kKT;
   const int n_rtiles = a.Qp / kRT;
@@ -941,16 +926,6 @@ static hipError_t launch_fast(const DenseArgs& args, hipStream_t stream) {
   if (few_rows) a.k_split = n_rtiles;
   a.k_pair = !few_rows && 2 * (int64_t)n_ktiles * BH > device_cus();
   const int k_slots = a.k_pair ? 3 * (n_ktiles / 2) + (n_ktiles & 1) : (few_rows ? n_ktiles : 2 * n_ktiles);
-  const int n_lim = (n_rows + 255) / 256;
-  const int64_t pairs = (int64_t)a.B * a.Q * a.H;
-  const int n_pre = (int)((pairs + 256 / (DP / 8) - 1) / (256 / (DP / 8)));
-  note_launch((const void*)&dense_bwd_prep_kernel<T, DP>,
-              {"dense_bwd_prep", dtype_code<T>(), DP, a.block, 256 / (DP / 8), DP, 4, 0, (unsigned)(n_lim + n_pre),
-               "rows"});
-  hipLaunchKernelGGL((dense_bwd_prep_kernel<T, DP>), dim3(n_lim + n_pre), dim3(256), 0, stream, a, n_lim,
-                     (int)(n_qtiles * BH), (int)(n_ktiles * BH));
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
   auto go = [&]<int LOGB>() {
     note_launch((const void*)&dense_bwd_dq_fast_kernel<T, DP, LOGB>,
                 {"dense_bwd_dq_fast", dtype_code<T>(), DP, 1 << LOGB, 128, 128, 4, 2, q_slots * BH,
