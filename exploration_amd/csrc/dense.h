@@ -19,8 +19,8 @@ struct DenseArgs {
   float* pr;              // [B,Q,H] remote probability mass
   float* zr;              // [B,Q,H] log Z_R (-inf: no remote block)
   float* z;               // [B,Q,H] logsumexp of all logits (-inf: padding)
-  float* delta;           // [B,Q,H] dO.O (backward workspace)
-  float* rho;             // [B,Q,H] dO.RC - delta*PR (backward workspace)
+  float* delta;           // [B,Q,H] dO.O (backward workspace, generic path)
+  float* rho;             // [B,Q,H] dO.RC - delta*PR (backward workspace, generic path)
   void* dq;               // [B,Q,H,D]
   void* dk;               // [B,N,H,D]
   void* dv;               // [B,N,H,D]
@@ -29,8 +29,8 @@ struct DenseArgs {
   int* tmin;              // [B,Qp/64] min of lim over 64-row tiles
   int* tmax;              // [B,Qp/64] max of lim over 64-row tiles
   float2* tab;            // [B*H, nblk, Qp] per (key block, row): (beta, eps)
-  // long work items run as two pieces whose fp32 partials a merge kernel
-  // adds afterwards (flags zeroed by the rows kernel)
+  // long work items run as pieces whose fp32 partials a merge kernel adds
+  // afterwards (each item's first piece writes its flag)
   int* q_count;           // [B*H*n_qtiles] 1 if the dQ item was split
   int* k_count;           // [B*H*n_ktiles] 1 if the dK/dV item was split
   float* q_part;          // dQ partials, [item][piece][wave][tile][register quad][lane] x 4
@@ -88,9 +88,11 @@ bool dense_fwd_fast_supported(int dtype, const DenseArgs& a);
 hipError_t launch_dense_fwd_fast(int dtype, const DenseArgs& a, hipStream_t stream);
 hipError_t launch_dense_bwd(int dtype, const DenseArgs& a, hipStream_t stream);
 
-// Workspace of the backward: delta and rho for every path, plus the row
-// limits, row-tile statistics and (beta, eps) table of the pipelined path
-// when it applies (16-bit, head_dim 64/128, table within its size cap).
+// Workspace of the backward: delta and rho (read by the generic path; the
+// pipelined dQ kernel computes them in registers, the space stays so that
+// one size formula serves both), plus the row limits, row-tile statistics,
+// (beta, eps) table, split flags and partials of the pipelined path when it
+// applies (16-bit, head_dim 64/128, table within its size cap).
 struct DenseBwdPlan {
   bool fast;
   int Qp, nblk, n_rtiles, n_qtiles, n_ktiles, q_pieces;
