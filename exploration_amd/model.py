@@ -15,6 +15,7 @@ identity here. The reference's differentiable sparse plumbing
 (``stack.py:333-383``), which it keeps for mathematical checks only, is not
 shipped: a gradient-enabled sparse forward raises ``ValueError``.
 """
+import contextlib
 import math
 import re
 from dataclasses import asdict, dataclass, fields
@@ -149,6 +150,59 @@ def _column_sum(t):
     return s if acc is None else s + acc
 
 
+# Weight casts of one training step under autocast without its cast cache
+# (the graph-captured step): None, or {id(weight): (weight, low-precision
+# copy)} while weights_cast_once() is active.
+_STEP_CASTS = {"cache": None}
+
+
+class _CastUse(torch.autograd.Function):
+    """One use of the step's shared low-precision copy of an fp32 weight, in
+    place of autocast's cast at that use: the forward returns the copy (the
+    same values as the cast), the backward hands this use's gradient to the
+    fp32 weight converted to fp32, which is what the cast's backward does. The
+    gradient's terms and their accumulation order are therefore those of a
+    cast at every use; only the cast kernels of the repeated uses (every
+    checkpointed chunk, forward and recompute) are gone."""
+
+    @staticmethod
+    def forward(ctx, low, weight):
+        return low.view_as(low)
+
+    @staticmethod
+    def backward(ctx, grad):
+        return None, grad.float()
+
+
+def _w(weight):
+    """A linear layer's weight at its use: inside ``weights_cast_once()``,
+    under autocast with gradients, the step's shared low-precision copy
+    (cast at the first use); otherwise the weight itself (autocast casts it)."""
+    cache = _STEP_CASTS["cache"]
+    if (cache is None or weight.dtype != torch.float32 or not torch.is_grad_enabled()
+            or not torch.is_autocast_enabled(weight.device.type)):
+        return weight
+    entry = cache.get(id(weight))
+    if entry is None or entry[0] is not weight:
+        entry = cache[id(weight)] = (weight, weight.detach().to(torch.get_autocast_dtype(weight.device.type)))
+    return _CastUse.apply(entry[1], weight)
+
+
+@contextlib.contextmanager
+def weights_cast_once():
+    """Scope of one training step (forward and backward, whose checkpointed
+    chunks recompute their forward): each fp32 weight is cast to the autocast
+    dtype once and every linear use reads that copy. For steps whose autocast
+    runs without its own cast cache (graph capture), which otherwise casts the
+    weight again at every use."""
+    previous = _STEP_CASTS["cache"]
+    _STEP_CASTS["cache"] = {}
+    try:
+        yield
+    finally:
+        _STEP_CASTS["cache"] = previous
+
+
 class _BiasAdd(torch.autograd.Function):
     """``y + b`` (b cast to y's dtype, as a fused linear bias under autocast);
     the bias gradient through ``_column_sum``."""
@@ -175,8 +229,8 @@ class FeedForward(nn.Sequential):
 
     def forward(self, x):
         fc1, act, fc2 = self
-        h = act(_BiasAdd.apply(F.linear(x, fc1.weight), fc1.bias))
-        return _BiasAdd.apply(F.linear(h, fc2.weight), fc2.bias)
+        h = act(_BiasAdd.apply(F.linear(x, _w(fc1.weight)), fc1.bias))
+        return _BiasAdd.apply(F.linear(h, _w(fc2.weight)), fc2.bias)
 
 
 def _window_attention(q, k, v, mask):
@@ -223,11 +277,11 @@ class HaloMemoryBlock(nn.Module):
                 raise ValueError("previous halo must contain exactly one block")
             first_key = max(0, start - b)
         seq = torch.cat((previous, F.pad(x, (0, 0, 0, groups * b - n))), 1)
-        qkv = self.qkv(self.attn_norm(seq))
+        qkv = F.linear(self.attn_norm(seq), _w(self.qkv.weight))
         if self.fused and halo_supported(qkv, b, self.hd):
             # rotary, window and attention in one kernel per direction
             ctx = halo_attention(qkv, self.rope, b, self.heads, n, start, first_key)
-            y = x + self.out(ctx)
+            y = x + F.linear(ctx, _w(self.out.weight))
             return y + self.ffn(self.ffn_norm(y))
         qkv = qkv.reshape(batch, groups + 1, b, 3, self.heads, self.hd)
         q, k, v = qkv.unbind(3)
@@ -239,7 +293,7 @@ class HaloMemoryBlock(nn.Module):
         key_pos = start + (torch.arange(groups, device=x.device)[:, None, None] - 1) * b + ko
         mask = (ko <= qo + b)[None] & (key_pos >= first_key) & (key_pos < start + n)
         ctx = _window_attention(q, kw, vw, mask[None]).reshape(batch, groups * b, dim)[:, :n]
-        y = x + self.out(ctx)
+        y = x + F.linear(ctx, _w(self.out.weight))
         return y + self.ffn(self.ffn_norm(y))
 
     def forward(self, x, positions=None, previous=None, start=0):
@@ -273,7 +327,8 @@ class KVProjection(nn.Module):
         ks, vs = [], []
         for lo in range(0, x.shape[1], self.chunk_tokens):
             sl = slice(lo, lo + self.chunk_tokens)
-            k, v = self.proj(self.norm(x[:, sl])).reshape(x.shape[0], -1, 2, self.heads, self.hd).unbind(2)
+            k, v = F.linear(self.norm(x[:, sl]), _w(self.proj.weight)).reshape(
+                x.shape[0], -1, 2, self.heads, self.hd).unbind(2)
             if self.use_rope:
                 k = self.rope(k, positions[sl])
             ks.append(k)
@@ -395,10 +450,10 @@ class StackModel(nn.Module):
     def _dense_round(self, rd, z, k, v, positions):
         """``stack.py:198-213``: q from z, the gated dense operator, readout and FFN."""
         def project(hidden):
-            return rd.wq(rd.q_norm(hidden))
+            return F.linear(rd.q_norm(hidden), _w(rd.wq.weight))
 
         def finish(hidden, context):
-            hidden = hidden + rd.read_out(context)
+            hidden = hidden + F.linear(context, _w(rd.read_out.weight))
             return hidden + rd.ffn(rd.ffn_norm(hidden))
 
         ckpt = self.checkpoint_chunks and torch.is_grad_enabled()
@@ -453,7 +508,7 @@ class StackModel(nn.Module):
         step = self._chunk_size(n)
 
         def head_loss(hidden, lab):
-            logits = self.lm_head(self.final_norm(hidden)).float()
+            logits = F.linear(self.final_norm(hidden), _w(self.lm_head.weight)).float()
             loss = F.cross_entropy(logits.flatten(0, 1), lab.flatten(), ignore_index=-100, reduction="sum")
             return loss, (logits.argmax(-1) == lab) | (lab == -100)
 

@@ -16,7 +16,11 @@ the update of every parameter and moment (and the step count) on the device.
 optimizer) into one HIP graph: the model's thousands of small kernels per
 step then cost one graph launch instead of as many launches from Python.
 """
+import contextlib
+
 import torch
+
+from .model import weights_cast_once
 
 
 def make_optimizer(model, lr=3e-4, weight_decay=0.01, capturable=False):
@@ -32,22 +36,27 @@ def train_step(model, optimizer, ids, targets, sup=None, clip_grad=1.0, precisio
     is skipped on the device (no host check) when the count is zero or the
     loss is not finite."""
     optimizer.zero_grad(set_to_none=True)
-    with torch.autocast(ids.device.type, dtype=torch.bfloat16, enabled=precision == "bf16",
-                        cache_enabled=autocast_cache):
-        result = model.forward_loss(ids, targets, sup, width=width)
-        count = result["count"]
-        if width is None and int(count) == 0:
-            raise ValueError("global batch has no supervised tokens")
-        loss = result["loss_sum"] / count
+    # without autocast's cast cache (graph capture), one cast per weight and
+    # step for forward and backward (the checkpointed chunks' recomputes)
+    with weights_cast_once() if not autocast_cache else contextlib.nullcontext():
+        with torch.autocast(ids.device.type, dtype=torch.bfloat16, enabled=precision == "bf16",
+                            cache_enabled=autocast_cache):
+            result = model.forward_loss(ids, targets, sup, width=width)
+            count = result["count"]
+            if width is None and int(count) == 0:
+                raise ValueError("global batch has no supervised tokens")
+            loss = result["loss_sum"] / count
+        if width is None:
+            if not bool(torch.isfinite(loss.detach())):
+                raise FloatingPointError("non-finite loss; optimizer step was not applied")
+            loss.backward()
+        else:
+            ok = (count > 0) & torch.isfinite(loss.detach())
+            loss.backward()
     if width is None:
-        if not bool(torch.isfinite(loss.detach())):
-            raise FloatingPointError("non-finite loss; optimizer step was not applied")
-        loss.backward()
         norm = torch.nn.utils.clip_grad_norm_(model.parameters(), clip_grad, error_if_nonfinite=True)
         optimizer.step()
         return loss.detach(), norm.detach(), count
-    ok = (count > 0) & torch.isfinite(loss.detach())
-    loss.backward()
     norm = torch.nn.utils.clip_grad_norm_(model.parameters(), clip_grad)
     if not _fused(optimizer):
         raise ValueError("a step without host checks needs the fused AdamW (make_optimizer on the GPU)")

@@ -277,3 +277,50 @@ def test_eager_step_guards_run_before_backward(monkeypatch):
     assert not opt.state
     for p, b in zip(m.parameters(), before):
         assert torch.equal(p.nan_to_num(), b.nan_to_num())
+
+
+def test_weights_cast_once_leaves_gradients_bitwise_unchanged():
+    """Under autocast without its cast cache (the graph-captured step), each
+    linear use casts its fp32 weight; weights_cast_once() casts each weight
+    once per step and hands every use's gradient back in fp32 instead. The
+    loss and every parameter gradient must be bitwise those of casting at
+    every use (checkpointed encoder chunks, read rounds and loss chunks
+    included), and each weight must be cast once."""
+    torch.manual_seed(0)
+    cfg = {"vocab_size": 64, "dim": 32, "heads": 2, "block_size": 4, "topk": 64, "arch": "Lx2,G", "ffn_ratio": 2.0}
+    m = M.build_model(cfg, execution={"checkpoint_chunks": True, "encoder_chunk": 16, "loss_chunk": 8})
+    ids = torch.randint(64, (2, 48))
+    targets = torch.roll(ids, -1, 1)
+
+    def grads(scope):
+        m.zero_grad(set_to_none=True)
+        with scope:
+            with torch.autocast("cpu", dtype=torch.bfloat16, cache_enabled=False):
+                loss = m.forward_loss(ids, targets)["loss_sum"]
+            loss.backward()
+        return loss.detach(), [p.grad.clone() for p in m.parameters()]
+
+    import contextlib
+
+    uses, copies = [], {}
+    real_apply = M._CastUse.apply
+
+    def counting_apply(low, weight):
+        uses.append(id(weight))
+        copies.setdefault(id(weight), low)
+        assert copies[id(weight)] is low  # every use of a weight reads the same copy
+        return real_apply(low, weight)
+
+    loss_ref, g_ref = grads(contextlib.nullcontext())
+    M._CastUse.apply = counting_apply
+    try:
+        loss_once, g_once = grads(M.weights_cast_once())
+    finally:
+        M._CastUse.apply = real_apply
+    assert torch.equal(loss_ref, loss_once)
+    for a, b in zip(g_ref, g_once):
+        assert a.dtype == torch.float32 and torch.equal(a, b)
+    weights = {id(p) for p in m.parameters() if p.ndim == 2 and p is not m.embedding.weight}
+    assert weights <= set(copies)              # every linear weight went through the copy
+    assert len(uses) > 2 * len(copies)         # and was used many times (chunks, recomputes)
+    assert M._STEP_CASTS["cache"] is None     # the scope is closed
