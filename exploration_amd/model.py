@@ -151,27 +151,45 @@ def _column_sum(t):
 
 
 # Weight casts of one training step under autocast without its cast cache
-# (the graph-captured step): None, or {id(weight): (weight, low-precision
-# copy)} while weights_cast_once() is active.
+# (the graph-captured step): None, or {id(weight): _StepWeight} while
+# weights_cast_once() is active.
 _STEP_CASTS = {"cache": None}
+
+
+class _StepWeight:
+    """An fp32 weight's low-precision copy for one step, and the fp32 sum of
+    its uses' gradients (``grad`` None until the first one arrives)."""
+
+    def __init__(self, weight):
+        self.weight = weight
+        self.low = weight.detach().to(torch.get_autocast_dtype(weight.device.type))
+        self.grad = None
 
 
 class _CastUse(torch.autograd.Function):
     """One use of the step's shared low-precision copy of an fp32 weight, in
-    place of autocast's cast at that use: the forward returns the copy (the
-    same values as the cast), the backward hands this use's gradient to the
-    fp32 weight converted to fp32, which is what the cast's backward does. The
-    gradient's terms and their accumulation order are therefore those of a
-    cast at every use; only the cast kernels of the repeated uses (every
-    checkpointed chunk, forward and recompute) are gone."""
+    place of autocast's cast at that use. The forward returns the copy (the
+    same values as the cast). The backward adds this use's gradient, in fp32,
+    to the weight's step sum: the first use's converted (``copy_``), each
+    later one added (``add_``), in the order the backward produces them. That
+    is the sum autograd forms of the casts' fp32 gradients (it keeps the first
+    and adds the others as they arrive), with one kernel per use instead of a
+    cast kernel plus an add; ``weights_cast_once`` hands the sum to the weight
+    as its gradient."""
 
     @staticmethod
-    def forward(ctx, low, weight):
+    def forward(ctx, low, weight, step):
+        ctx.step = step
         return low.view_as(low)
 
     @staticmethod
     def backward(ctx, grad):
-        return None, grad.float()
+        step = ctx.step
+        if step.grad is None:
+            step.grad = torch.empty_like(step.weight).copy_(grad)
+        else:
+            step.grad.add_(grad)
+        return None, None, None
 
 
 def _w(weight):
@@ -182,23 +200,30 @@ def _w(weight):
     if (cache is None or weight.dtype != torch.float32 or not torch.is_grad_enabled()
             or not torch.is_autocast_enabled(weight.device.type)):
         return weight
-    entry = cache.get(id(weight))
-    if entry is None or entry[0] is not weight:
-        entry = cache[id(weight)] = (weight, weight.detach().to(torch.get_autocast_dtype(weight.device.type)))
-    return _CastUse.apply(entry[1], weight)
+    step = cache.get(id(weight))
+    if step is None or step.weight is not weight:
+        step = cache[id(weight)] = _StepWeight(weight)
+    return _CastUse.apply(step.low, weight, step)
 
 
 @contextlib.contextmanager
 def weights_cast_once():
     """Scope of one training step (forward and backward, whose checkpointed
     chunks recompute their forward): each fp32 weight is cast to the autocast
-    dtype once and every linear use reads that copy. For steps whose autocast
-    runs without its own cast cache (graph capture), which otherwise casts the
-    weight again at every use."""
+    dtype once and every linear use reads that copy; on leaving the scope the
+    uses' fp32 gradient sum becomes the weight's gradient (added before any
+    gradient autograd gave the weight directly: the embedding's, whose
+    backward runs after every use of the tied output weight). For steps whose
+    autocast runs without its own cast cache (graph capture), which otherwise
+    casts the weight again at every use."""
     previous = _STEP_CASTS["cache"]
-    _STEP_CASTS["cache"] = {}
+    cache = _STEP_CASTS["cache"] = {}
     try:
         yield
+        for step in cache.values():
+            if step.grad is not None:
+                w = step.weight
+                w.grad = step.grad if w.grad is None else step.grad.add_(w.grad)
     finally:
         _STEP_CASTS["cache"] = previous
 

@@ -282,10 +282,11 @@ def test_eager_step_guards_run_before_backward(monkeypatch):
 def test_weights_cast_once_leaves_gradients_bitwise_unchanged():
     """Under autocast without its cast cache (the graph-captured step), each
     linear use casts its fp32 weight; weights_cast_once() casts each weight
-    once per step and hands every use's gradient back in fp32 instead. The
-    loss and every parameter gradient must be bitwise those of casting at
-    every use (checkpointed encoder chunks, read rounds and loss chunks
-    included), and each weight must be cast once."""
+    once per step and sums the uses' gradients in fp32 itself. The loss and
+    every parameter gradient (the tied embedding / output weight included)
+    must be bitwise those of casting at every use (checkpointed encoder
+    chunks, read rounds and loss chunks included), and each weight must be
+    cast once."""
     torch.manual_seed(0)
     cfg = {"vocab_size": 64, "dim": 32, "heads": 2, "block_size": 4, "topk": 64, "arch": "Lx2,G", "ffn_ratio": 2.0}
     m = M.build_model(cfg, execution={"checkpoint_chunks": True, "encoder_chunk": 16, "loss_chunk": 8})
@@ -305,11 +306,11 @@ def test_weights_cast_once_leaves_gradients_bitwise_unchanged():
     uses, copies = [], {}
     real_apply = M._CastUse.apply
 
-    def counting_apply(low, weight):
+    def counting_apply(low, weight, step):
         uses.append(id(weight))
         copies.setdefault(id(weight), low)
         assert copies[id(weight)] is low  # every use of a weight reads the same copy
-        return real_apply(low, weight)
+        return real_apply(low, weight, step)
 
     loss_ref, g_ref = grads(contextlib.nullcontext())
     M._CastUse.apply = counting_apply
