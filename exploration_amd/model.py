@@ -327,14 +327,21 @@ class HaloMemoryBlock(nn.Module):
         step = self.query_chunk_size * self.block_size
         b = self.block_size
         outs = []
-        for lo in range(0, x.shape[1], step):
-            hi = min(lo + step, x.shape[1])
-            prev = previous if lo == 0 else x[:, lo - b:lo]
+        # the chunks as one split of x (its backward is one concatenation; a
+        # basic slice per chunk would make every chunk's backward a
+        # zero-filled x-sized gradient, added up over the chunks). The halo
+        # block stays a slice of x, which keeps the gradient's sums exactly
+        # those of slicing every chunk (a slice of the previous piece sums
+        # them in another order).
+        pieces = x.split(step, 1) if x.shape[1] > step else (x,)
+        for i, piece in enumerate(pieces):
+            lo = i * step
+            prev = previous if i == 0 else x[:, lo - b:lo]
             if self.checkpoint_chunks and torch.is_grad_enabled():
-                outs.append(checkpoint(self.forward_chunk, x[:, lo:hi], prev, start + lo, use_reentrant=False,
+                outs.append(checkpoint(self.forward_chunk, piece, prev, start + lo, use_reentrant=False,
                                        preserve_rng_state=False))
             else:
-                outs.append(self.forward_chunk(x[:, lo:hi], prev, start + lo))
+                outs.append(self.forward_chunk(piece, prev, start + lo))
         return torch.cat(outs, 1)
 
 
@@ -531,6 +538,12 @@ class StackModel(nn.Module):
         x, k, v = self.encode(input_ids, offset)
         losses, hits = [], []
         step = self._chunk_size(n)
+        # the supervised rows in slot order, gathered once and split into
+        # the read chunks (backward: one scatter-add into a zero-filled x
+        # gradient and one concatenation, instead of both per chunk; advanced
+        # indexing's backward sorts and runs a look-back unique pass)
+        rows = torch.gather(x, 1, safe[:, :, None].expand(-1, -1, x.shape[-1]))
+        rows = rows.split(step, 1) if width > step else (rows,)
 
         def head_loss(hidden, lab):
             logits = F.linear(self.final_norm(hidden), _w(self.lm_head.weight)).float()
@@ -539,9 +552,7 @@ class StackModel(nn.Module):
 
         for lo in range(0, width, step):
             hi = min(lo + step, width)
-            # gather rows (backward: scatter-add; advanced indexing's backward
-            # sorts and runs a look-back unique pass)
-            z = torch.gather(x, 1, safe[:, lo:hi, None].expand(-1, -1, x.shape[-1]))
+            z = rows[lo // step]
             for rd in self.reads:
                 z = self._dense_round(rd, z, k, v, pos[:, lo:hi])
             for j in range(0, hi - lo, self.loss_chunk):
