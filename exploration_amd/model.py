@@ -329,14 +329,19 @@ class HaloMemoryBlock(nn.Module):
         outs = []
         # the chunks as one split of x (its backward is one concatenation; a
         # basic slice per chunk would make every chunk's backward a
-        # zero-filled x-sized gradient, added up over the chunks). The halo
-        # block stays a slice of x, which keeps the gradient's sums exactly
-        # those of slicing every chunk (a slice of the previous piece sums
-        # them in another order).
+        # zero-filled x-sized gradient, added up over the chunks), and the
+        # halo blocks (the last block of every chunk but the last) as one
+        # copy of a strided view of x, so that all of them cost one x-sized
+        # gradient in backward. Both keep the gradient's sums exactly those of
+        # slicing every chunk and halo (a slice of the previous piece would
+        # sum them in another order).
         pieces = x.split(step, 1) if x.shape[1] > step else (x,)
+        if len(pieces) > 1:
+            halos = x[:, :(len(pieces) - 1) * step].unflatten(1, (len(pieces) - 1, step))[:, :, step - b:]
+            halos = halos.contiguous()
         for i, piece in enumerate(pieces):
             lo = i * step
-            prev = previous if i == 0 else x[:, lo - b:lo]
+            prev = previous if i == 0 else halos[:, i - 1]
             if self.checkpoint_chunks and torch.is_grad_enabled():
                 outs.append(checkpoint(self.forward_chunk, piece, prev, start + lo, use_reentrant=False,
                                        preserve_rng_state=False))
