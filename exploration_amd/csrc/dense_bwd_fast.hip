@@ -926,6 +926,9 @@ static hipError_t launch_fast(const DenseArgs& args, hipStream_t stream) {
   if (few_rows) a.k_split = n_rtiles;
   a.k_pair = !few_rows && 2 * (int64_t)n_ktiles * BH > device_cus();
   const int k_slots = a.k_pair ? 3 * (n_ktiles / 2) + (n_ktiles & 1) : (few_rows ? n_ktiles : 2 * n_ktiles);
+  // merge workgroups: the dQ items, then the dK/dV items unless none can be
+  // split (few rows)
+  const unsigned merge_items = (unsigned)((n_qtiles + (few_rows ? 0 : n_ktiles)) * BH);
   auto go = [&]<int LOGB>() {
     note_launch((const void*)&dense_bwd_dq_fast_kernel<T, DP, LOGB>,
                 {"dense_bwd_dq_fast", dtype_code<T>(), DP, 1 << LOGB, 128, 128, 4, 2, q_slots * BH,
@@ -935,14 +938,14 @@ static hipError_t launch_fast(const DenseArgs& args, hipStream_t stream) {
                  a.k_pair ? "pair" : "slot"});
     note_launch((const void*)&dense_bwd_merge_kernel<T, DP>,
                 {"dense_bwd_merge", dtype_code<T>(), DP, 1 << LOGB, 128, DP, 4, 0,
-                 (unsigned)((n_qtiles + n_ktiles) * BH * 2 * (DP / 32)), "rows"});
+                 merge_items * 2 * (DP / 32), "rows"});
     hipLaunchKernelGGL((dense_bwd_dq_fast_kernel<T, DP, LOGB>), dim3(q_slots * BH), dim3(256), 0, stream,
                        a, n_qtiles);
     if (hipPeekAtLastError() != hipSuccess) return;
     hipLaunchKernelGGL((dense_bwd_dkv_fast_kernel<T, DP, LOGB>), dim3(k_slots * BH), dim3(256), 0,
                        stream, a, n_rtiles, n_ktiles);
     if (hipPeekAtLastError() != hipSuccess) return;
-    hipLaunchKernelGGL((dense_bwd_merge_kernel<T, DP>), dim3((n_qtiles + n_ktiles) * BH, 2 * (DP / 32)),
+    hipLaunchKernelGGL((dense_bwd_merge_kernel<T, DP>), dim3(merge_items, 2 * (DP / 32)),
                        dim3(256), 0, stream, a, n_qtiles, n_ktiles);
   };
   switch (a.logb) {
