@@ -388,27 +388,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }(std::make_integer_sequence<int, NST>{});
     expo.template operator()<NST - 1, 0>();
     expo.template operator()<NST - 1, 1>();
-    // U_j, then direct = P (dP - delta) with P = u U_j e^{ZR-Z} (remote) or u
-    float ub[NST][8];
+    // U_j and X_j = sum u_i dP_i per block. With m_j = P_i / u_i (U_j
+    // e^{ZR-Z} remote, 1 local), G_j = m_j (X_j - delta U_j), so the gate
+    // coefficient G_j / U_j - rho is e^{ZR-Z} (X_j - delta U_j) - rho on
+    // remote blocks (0 where U_j = 0: every u is 0) and 0 on local ones, and
+    //   dA_i = P_i (dP_i - delta) + u_i gb_j = u_i (m_j dP_i + c_j),
+    //   c_j = gb_j - m_j delta.
+    float ub[NST][8], xb[NST][8];
     block_sums<NST, LOGB>(s, ub);
-    float mult[NST][NS];
+    block_dots<NST, LOGB>(s, dp, xb);
+    float mult[NST][NS], cb[NST][NS], gb[NST][8];
 #pragma unroll
     for (int st = 0; st < NST; ++st)
 #pragma unroll
-      for (int j = 0; j < NS; ++j) mult[st][j] = remb[st][j] ? ub[st][j] * ezrz : 1.f;
-#pragma unroll
-    for (int st = 0; st < NST; ++st)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) dp[st][r] = s[st][r] * mult[st][blk_slot<LOGB>(r)] * (dp[st][r] - dl);
-    float gb[NST][8];
-    block_sums<NST, LOGB>(dp, gb);
-    // gate coefficient per block: G_j / U_j - rho on remote blocks (0 where
-    // U_j = 0: every u is 0), 0 on local ones
-#pragma unroll
-    for (int st = 0; st < NST; ++st)
-#pragma unroll
-      for (int j = 0; j < NS; ++j)
-        gb[st][j] = remb[st][j] && ub[st][j] > 0.f ? gb[st][j] / ub[st][j] - rho : 0.f;
+      for (int j = 0; j < NS; ++j) {
+        mult[st][j] = remb[st][j] ? ub[st][j] * ezrz : 1.f;
+        gb[st][j] = remb[st][j] && ub[st][j] > 0.f ? ezrz * fmaf(-dl, ub[st][j], xb[st][j]) - rho : 0.f;
+        cb[st][j] = fmaf(-mult[st][j], dl, gb[st][j]);
+      }
     // table entries of this tile's blocks (one writer per row and block)
     if (row_in && (BlkSlots<LOGB>::per_half || half == 0)) {
       constexpr int STEP = LOGB >= 5 ? ((1 << LOGB) / 32 < NST ? (1 << LOGB) / 32 : NST) : 1;
@@ -440,7 +437,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     Frag bd[NST][2];
     auto gate = [&]<int ST>() {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dp[ST][r] = fmaf(s[ST][r], gb[ST][blk_slot<LOGB>(r)], dp[ST][r]);
+      for (int r = 0; r < 16; ++r)
+        dp[ST][r] = s[ST][r] * fmaf(mult[ST][blk_slot<LOGB>(r)], dp[ST][r], cb[ST][blk_slot<LOGB>(r)]);
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2) bd[ST][h2] = frag_from_c<T>(dp[ST], h2);
     };

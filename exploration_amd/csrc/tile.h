@@ -218,6 +218,60 @@ __device__ __forceinline__ void block_sums(const f32x16 (&x)[NST], float (&blk)[
   }
 }
 
+// Per-(row, key block) sums of x*y, in the layout of block_sums; the in-lane
+// part is a chain of FMAs (one instruction per element).
+template <int NST, int LOGB>
+__device__ __forceinline__ void block_dots(const f32x16 (&x)[NST], const f32x16 (&y)[NST], float (&blk)[NST][8]) {
+  if constexpr ((1 << LOGB) > 32 * NST) {
+    // block larger than the tile: never dispatched (tiles hold whole blocks)
+  } else if constexpr (LOGB >= 5) {
+    constexpr int G = (1 << LOGB) / 32;  // subtiles per block
+    float t[NST];
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+      float acc = x[st][0] * y[st][0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) acc = fmaf(x[st][r], y[st][r], acc);
+      t[st] = acc;
+    }
+#pragma unroll
+    for (int st = 0; st < NST; ++st) t[st] += other_half(t[st]);
+#pragma unroll
+    for (int g0 = 0; g0 < NST; g0 += G) {
+      float tot = t[g0];
+#pragma unroll
+      for (int g = 1; g < G; ++g) tot += t[g0 + g];
+#pragma unroll
+      for (int g = 0; g < G; ++g) blk[g0 + g][0] = tot;
+    }
+  } else if constexpr (LOGB == 4) {
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+      float a0 = x[st][0] * y[st][0], a1 = x[st][8] * y[st][8];
+#pragma unroll
+      for (int r = 1; r < 8; ++r) { a0 = fmaf(x[st][r], y[st][r], a0); a1 = fmaf(x[st][r + 8], y[st][r + 8], a1); }
+      blk[st][0] = a0 + other_half(a0);
+      blk[st][1] = a1 + other_half(a1);
+    }
+  } else if constexpr (LOGB == 3 || LOGB == 2) {
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float a = x[st][4 * i] * y[st][4 * i];
+#pragma unroll
+        for (int e = 1; e < 4; ++e) a = fmaf(x[st][4 * i + e], y[st][4 * i + e], a);
+        blk[st][i] = LOGB == 3 ? a + other_half(a) : a;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int st = 0; st < NST; ++st)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) blk[st][i] = fmaf(x[st][2 * i + 1], y[st][2 * i + 1], x[st][2 * i] * y[st][2 * i]);
+  }
+}
+
 // Index, within the tile, of the key block that slot j of subtile st in a
 // lane of half h refers to (block size 2^LOGB, NST subtiles of 32 keys).
 template <int LOGB> __device__ __forceinline__ int blk_index(int st, int j, int h) {
