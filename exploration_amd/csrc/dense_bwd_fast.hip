@@ -372,8 +372,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         else s[ST][r] = offset(ST, r) < lim_v ? fast_exp2(x) : 0.f;
       }
     };
+    // in-lane parts of U_j (sums of u) and X_j (sums of u dP) of subtile ST
+    float up[NST][8], xp[NST][8];
+    auto part = [&]<int ST>() {
+      block_part<LOGB, false>(s[ST], s[ST], up[ST]);
+      block_part<LOGB, true>(s[ST], dp[ST], xp[ST]);
+    };
     // S^T = K Q^T and dP^T = V dO^T of subtile ST: product j is chunk j/2,
-    // S (even j) or dP (odd j); the exponentials of subtile ST-1 overlap them
+    // S (even j) or dP (odd j); the exponentials and in-lane sums of subtile
+    // ST-1 overlap them
     auto p1 = [&]<int ST>() {
       auto load = [&](int j) { return rfrag((j & 1) ? vt : kt, ST, j >> 1); };
       auto mma = [&](int j, Frag f) {
@@ -381,13 +388,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         else s[ST] = M::mma(f, qf[j >> 1], s[ST]);
       };
       if constexpr (ST == 0) mfma_phase<2 * NKC, 4, 1>(load, mma);
-      else mfma_phase_overlap<2 * NKC, 4, 1, 2>(load, mma, [&]<int K>() { expo.template operator()<ST - 1, K>(); });
+      else
+        mfma_phase_overlap<2 * NKC, 4, 1, 3>(load, mma, [&]<int K>() {
+          if constexpr (K < 2) expo.template operator()<ST - 1, K>();
+          else part.template operator()<ST - 1>();
+        });
     };
     [&]<int... ST>(std::integer_sequence<int, ST...>) {
       (p1.template operator()<ST>(), ...);
     }(std::make_integer_sequence<int, NST>{});
     expo.template operator()<NST - 1, 0>();
     expo.template operator()<NST - 1, 1>();
+    part.template operator()<NST - 1>();
     // U_j and X_j = sum u_i dP_i per block. With m_j = P_i / u_i (U_j
     // e^{ZR-Z} remote, 1 local), G_j = m_j (X_j - delta U_j), so the gate
     // coefficient G_j / U_j - rho is e^{ZR-Z} (X_j - delta U_j) - rho on
@@ -395,8 +407,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     //   dA_i = P_i (dP_i - delta) + u_i gb_j = u_i (m_j dP_i + c_j),
     //   c_j = gb_j - m_j delta.
     float ub[NST][8], xb[NST][8];
-    block_sums<NST, LOGB>(s, ub);
-    block_dots<NST, LOGB>(s, dp, xb);
+    block_finish<NST, LOGB>(up, ub);
+    block_finish<NST, LOGB>(xp, xb);
     float mult[NST][NS], cb[NST][NS], gb[NST][8];
 #pragma unroll
     for (int st = 0; st < NST; ++st)

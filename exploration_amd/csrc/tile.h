@@ -218,24 +218,49 @@ __device__ __forceinline__ void block_sums(const f32x16 (&x)[NST], float (&blk)[
   }
 }
 
-// Per-(row, key block) sums of x*y, in the layout of block_sums; the in-lane
-// part is a chain of FMAs (one instruction per element).
+// block_sums in two parts, so that the in-lane part of one subtile can run
+// beside the MFMAs of the next. block_part: this lane's slot sums of one C
+// tile (of x, or with DOT of x*y as a chain of FMAs, one instruction per
+// element); block_finish: the other half-wave's part (blocks of 8+ keys)
+// and, for blocks of several subtiles, their total.
+template <int LOGB, bool DOT>
+__device__ __forceinline__ void block_part(const f32x16& x, const f32x16& y, float (&part)[8]) {
+  auto first = [&](int r) { return DOT ? x[r] * y[r] : x[r]; };
+  auto next = [&](float a, int r) { return DOT ? fmaf(x[r], y[r], a) : a + x[r]; };
+  if constexpr (LOGB >= 5) {
+    float a = first(0);
+#pragma unroll
+    for (int r = 1; r < 16; ++r) a = next(a, r);
+    part[0] = a;
+  } else if constexpr (LOGB == 4) {
+    float a0 = first(0), a1 = first(8);
+#pragma unroll
+    for (int r = 1; r < 8; ++r) { a0 = next(a0, r); a1 = next(a1, r + 8); }
+    part[0] = a0;
+    part[1] = a1;
+  } else if constexpr (LOGB >= 2) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float a = first(4 * i);
+#pragma unroll
+      for (int e = 1; e < 4; ++e) a = next(a, 4 * i + e);
+      part[i] = a;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) part[i] = next(first(2 * i), 2 * i + 1);
+  }
+}
+
 template <int NST, int LOGB>
-__device__ __forceinline__ void block_dots(const f32x16 (&x)[NST], const f32x16 (&y)[NST], float (&blk)[NST][8]) {
+__device__ __forceinline__ void block_finish(const float (&part)[NST][8], float (&blk)[NST][8]) {
   if constexpr ((1 << LOGB) > 32 * NST) {
     // block larger than the tile: never dispatched (tiles hold whole blocks)
   } else if constexpr (LOGB >= 5) {
     constexpr int G = (1 << LOGB) / 32;  // subtiles per block
     float t[NST];
 #pragma unroll
-    for (int st = 0; st < NST; ++st) {
-      float acc = x[st][0] * y[st][0];
-#pragma unroll
-      for (int r = 1; r < 16; ++r) acc = fmaf(x[st][r], y[st][r], acc);
-      t[st] = acc;
-    }
-#pragma unroll
-    for (int st = 0; st < NST; ++st) t[st] += other_half(t[st]);
+    for (int st = 0; st < NST; ++st) t[st] = part[st][0] + other_half(part[st][0]);
 #pragma unroll
     for (int g0 = 0; g0 < NST; g0 += G) {
       float tot = t[g0];
@@ -244,31 +269,12 @@ __device__ __forceinline__ void block_dots(const f32x16 (&x)[NST], const f32x16 
 #pragma unroll
       for (int g = 0; g < G; ++g) blk[g0 + g][0] = tot;
     }
-  } else if constexpr (LOGB == 4) {
-#pragma unroll
-    for (int st = 0; st < NST; ++st) {
-      float a0 = x[st][0] * y[st][0], a1 = x[st][8] * y[st][8];
-#pragma unroll
-      for (int r = 1; r < 8; ++r) { a0 = fmaf(x[st][r], y[st][r], a0); a1 = fmaf(x[st][r + 8], y[st][r + 8], a1); }
-      blk[st][0] = a0 + other_half(a0);
-      blk[st][1] = a1 + other_half(a1);
-    }
-  } else if constexpr (LOGB == 3 || LOGB == 2) {
-#pragma unroll
-    for (int st = 0; st < NST; ++st) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float a = x[st][4 * i] * y[st][4 * i];
-#pragma unroll
-        for (int e = 1; e < 4; ++e) a = fmaf(x[st][4 * i + e], y[st][4 * i + e], a);
-        blk[st][i] = LOGB == 3 ? a + other_half(a) : a;
-      }
-    }
   } else {
+    constexpr int NSL = LOGB == 4 ? 2 : (LOGB >= 2 ? 4 : 8);  // slots per subtile
 #pragma unroll
     for (int st = 0; st < NST; ++st)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) blk[st][i] = fmaf(x[st][2 * i + 1], y[st][2 * i + 1], x[st][2 * i] * y[st][2 * i]);
+      for (int j = 0; j < NSL; ++j) blk[st][j] = LOGB >= 3 ? part[st][j] + other_half(part[st][j]) : part[st][j];
   }
 }
 
