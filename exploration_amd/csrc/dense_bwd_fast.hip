@@ -378,75 +378,57 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       block_part<LOGB, false>(s[ST], s[ST], up[ST]);
       block_part<LOGB, true>(s[ST], dp[ST], xp[ST]);
     };
-    // S^T = K Q^T and dP^T = V dO^T of subtile ST: product j is chunk j/2,
-    // S (even j) or dP (odd j); the exponentials and in-lane sums of subtile
-    // ST-1 overlap them
-    auto p1 = [&]<int ST>() {
-      auto load = [&](int j) { return rfrag((j & 1) ? vt : kt, ST, j >> 1); };
-      auto mma = [&](int j, Frag f) {
-        if (j & 1) dp[ST] = M::mma(f, gf[j >> 1], dp[ST]);
-        else s[ST] = M::mma(f, qf[j >> 1], s[ST]);
-      };
-      if constexpr (ST == 0) mfma_phase<2 * NKC, 4, 1>(load, mma);
-      else
-        mfma_phase_overlap<2 * NKC, 4, 1, 3>(load, mma, [&]<int K>() {
-          if constexpr (K < 2) expo.template operator()<ST - 1, K>();
-          else part.template operator()<ST - 1>();
-        });
-    };
-    [&]<int... ST>(std::integer_sequence<int, ST...>) {
-      (p1.template operator()<ST>(), ...);
-    }(std::make_integer_sequence<int, NST>{});
-    expo.template operator()<NST - 1, 0>();
-    expo.template operator()<NST - 1, 1>();
-    part.template operator()<NST - 1>();
-    // U_j and X_j = sum u_i dP_i per block. With m_j = P_i / u_i (U_j
+    // The tile's finish, once the last subtile's in-lane sums are in: U_j
+    // and X_j = sum u_i dP_i per block, the multipliers, the gate
+    // coefficients and the table entries. With m_j = P_i / u_i (U_j
     // e^{ZR-Z} remote, 1 local), G_j = m_j (X_j - delta U_j), so the gate
     // coefficient G_j / U_j - rho is e^{ZR-Z} (X_j - delta U_j) - rho on
     // remote blocks (0 where U_j = 0: every u is 0) and 0 on local ones, and
     //   dA_i = P_i (dP_i - delta) + u_i gb_j = u_i (m_j dP_i + c_j),
     //   c_j = gb_j - m_j delta.
-    float ub[NST][8], xb[NST][8];
-    block_finish<NST, LOGB>(up, ub);
-    block_finish<NST, LOGB>(xp, xb);
-    float mult[NST][NS], cb[NST][NS], gb[NST][8];
+    float mult[NST][NS], cb[NST][NS];
+    Frag bd[NST][2];
+    auto finish = [&]() {
+      float ub[NST][8], xb[NST][8], gb[NST][8];
+      block_finish<NST, LOGB>(up, ub);
+      block_finish<NST, LOGB>(xp, xb);
 #pragma unroll
-    for (int st = 0; st < NST; ++st)
-#pragma unroll
-      for (int j = 0; j < NS; ++j) {
-        mult[st][j] = remb[st][j] ? ub[st][j] * ezrz : 1.f;
-        gb[st][j] = remb[st][j] && ub[st][j] > 0.f ? ezrz * fmaf(-dl, ub[st][j], xb[st][j]) - rho : 0.f;
-        cb[st][j] = fmaf(-mult[st][j], dl, gb[st][j]);
-      }
-    // table entries of this tile's blocks (one writer per row and block)
-    if (row_in && (BlkSlots<LOGB>::per_half || half == 0)) {
-      constexpr int STEP = LOGB >= 5 ? ((1 << LOGB) / 32 < NST ? (1 << LOGB) / 32 : NST) : 1;
-#pragma unroll
-      for (int st = 0; st < NST; st += STEP)
+      for (int st = 0; st < NST; ++st)
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
-          const int bl = (kb >> LOGB) + blk_index<LOGB>(st, j, half);
-          const int ks = bl << LOGB;
-          float beta, eps;
-          if (FULL || ks < rlim) {
-            const float u = ub[st][j];
-            beta = base_l - fast_log2(u);
-            const float w = u * ezrz;
-            float gam = w > 0.f ? gb[st][j] / w : 0.f;
-            gam = fabsf(gam) <= 3.0e38f ? gam : 0.f;  // overflow only where P_i is 0
-            eps = gam - dl;
-          } else if (ks <= lhi) {
-            beta = base_l;
-            eps = -dl;
-          } else {
-            beta = kInf;
-            eps = 0.f;
-          }
-          tab[(int64_t)bl * a.Qp + row] = make_float2(beta, eps);
+          mult[st][j] = remb[st][j] ? ub[st][j] * ezrz : 1.f;
+          gb[st][j] = remb[st][j] && ub[st][j] > 0.f ? ezrz * fmaf(-dl, ub[st][j], xb[st][j]) - rho : 0.f;
+          cb[st][j] = fmaf(-mult[st][j], dl, gb[st][j]);
         }
-    }
+      // table entries of this tile's blocks (one writer per row and block)
+      if (row_in && (BlkSlots<LOGB>::per_half || half == 0)) {
+        constexpr int STEP = LOGB >= 5 ? ((1 << LOGB) / 32 < NST ? (1 << LOGB) / 32 : NST) : 1;
+#pragma unroll
+        for (int st = 0; st < NST; st += STEP)
+#pragma unroll
+          for (int j = 0; j < NS; ++j) {
+            const int bl = (kb >> LOGB) + blk_index<LOGB>(st, j, half);
+            const int ks = bl << LOGB;
+            float beta, eps;
+            if (FULL || ks < rlim) {
+              const float u = ub[st][j];
+              beta = base_l - fast_log2(u);
+              const float w = u * ezrz;
+              float gam = w > 0.f ? gb[st][j] / w : 0.f;
+              gam = fabsf(gam) <= 3.0e38f ? gam : 0.f;  // overflow only where P_i is 0
+              eps = gam - dl;
+            } else if (ks <= lhi) {
+              beta = base_l;
+              eps = -dl;
+            } else {
+              beta = kInf;
+              eps = 0.f;
+            }
+            tab[(int64_t)bl * a.Qp + row] = make_float2(beta, eps);
+          }
+      }
+    };
     // dA of subtile ST (direct + gate term) as 16-bit MFMA operands
-    Frag bd[NST][2];
     auto gate = [&]<int ST>() {
 #pragma unroll
       for (int r = 0; r < 16; ++r)
@@ -454,18 +436,63 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2) bd[ST][h2] = frag_from_c<T>(dp[ST], h2);
     };
-    // dQ^T += K^T dA^T over the keys of subtile ST: product j is 16-key chunk
-    // 2ST + j/NDT, head-dim tile j % NDT; subtile ST+1's gate overlaps them
-    auto p2 = [&]<int ST>() {
-      auto load = [&](int j) { return tfrag(kt, 16 * (2 * ST + j / NDT), j % NDT); };
-      auto mma = [&](int j, Frag f) { acc[j % NDT] = M::mma(f, bd[ST][j / NDT], acc[j % NDT]); };
-      if constexpr (ST + 1 < NST) mfma_phase_overlap<2 * NDT, 4, 2, 1>(load, mma, [&]<int K>() { gate.template operator()<ST + 1>(); });
-      else mfma_phase<2 * NDT, 4, 2>(load, mma);
+    // One chain of products per tile, one chunk (4 MFMAs) of LDS reads
+    // ahead throughout: S^T = K Q^T and dP^T = V dO^T of each subtile (2 NKC
+    // products, S even, dP odd), then dQ^T += K^T dA^T (2 NDT products per
+    // subtile: 16-key chunk 2ST + k/NDT, head-dim tile k % NDT). Beside the
+    // S/dP products of subtile ST run the exponentials and in-lane sums of
+    // subtile ST-1; after the last ones, the tile's finish and the first
+    // gate (the reads of the first dQ chunk already in flight); beside the
+    // dQ products of subtile ST, the gate of subtile ST+1.
+    constexpr int P1 = 2 * NKC, P2 = 2 * NDT, N1 = NST * P1;
+    constexpr int CP1 = P1 / 4, CP2 = P2 / 4, C1 = NST * CP1, C2 = NST * CP2;
+    static_assert(P1 % 4 == 0 && P2 % 4 == 0, "whole chunks per subtile");
+    auto load = [&]<int J>() -> Frag {
+      if constexpr (J < N1) {
+        constexpr int st = J / P1, jj = J % P1;
+        return rfrag((jj & 1) ? vt : kt, st, jj >> 1);
+      } else {
+        constexpr int jj = J - N1, st = jj / P2, k = jj % P2;
+        return tfrag(kt, 16 * (2 * st + k / NDT), k % NDT);
+      }
     };
-    gate.template operator()<0>();
-    [&]<int... ST>(std::integer_sequence<int, ST...>) {
-      (p2.template operator()<ST>(), ...);
-    }(std::make_integer_sequence<int, NST>{});
+    auto mma = [&]<int J>(Frag f) {
+      if constexpr (J < N1) {
+        constexpr int st = J / P1, jj = J % P1;
+        if constexpr (jj & 1) dp[st] = M::mma(f, gf[jj >> 1], dp[st]);
+        else s[st] = M::mma(f, qf[jj >> 1], s[st]);
+      } else {
+        constexpr int jj = J - N1, st = jj / P2, k = jj % P2;
+        acc[k % NDT] = M::mma(f, bd[st][k / NDT], acc[k % NDT]);
+      }
+    };
+    auto after = [&]<int G>() {
+      if constexpr (G < C1) {
+        constexpr int st = G / CP1, lg = G % CP1;
+        if constexpr (st >= 1) {
+          // slices [lg*3/CP1, (lg+1)*3/CP1) of subtile st-1: the two halves
+          // of its exponentials, then its in-lane sums
+          [&]<int... K>(std::integer_sequence<int, K...>) {
+            ([&] {
+              constexpr int k = lg * 3 / CP1 + K;
+              if constexpr (k < 2) expo.template operator()<st - 1, k>();
+              else part.template operator()<st - 1>();
+            }(), ...);
+          }(std::make_integer_sequence<int, (lg + 1) * 3 / CP1 - lg * 3 / CP1>{});
+        }
+        if constexpr (G == C1 - 1) {
+          expo.template operator()<NST - 1, 0>();
+          expo.template operator()<NST - 1, 1>();
+          part.template operator()<NST - 1>();
+          finish();
+          gate.template operator()<0>();
+        }
+      } else {
+        constexpr int st = (G - C1) / CP2, lg = (G - C1) % CP2;
+        if constexpr (lg == CP2 - 1 && st + 1 < NST) gate.template operator()<st + 1>();
+      }
+    };
+    mfma_chain<C1 + C2, 4>(load, mma, after);
   };
   auto run = [&]<int BUF>(int i) {
     if (i < full) step.template operator()<BUF, true>(i);
@@ -767,37 +794,50 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 
         }
       }
     };
-    // S = Q K^T and dP = dO V^T of row subtile RS: product j is chunk j/2,
-    // S (even j) or dP (odd j)
-    auto p1_load = [&]<int RS>(int j) { return rfrag((j & 1) ? gt : qt, RS, j >> 1); };
-    auto p1_mma = [&]<int RS>(int j, Frag f) {
-      if (j & 1) dp[RS] = M::mma(f, vf[j >> 1], dp[RS]);
-      else s[RS] = M::mma(f, kf[j >> 1], s[RS]);
-    };
-    // dV^T += dO^T P and dK^T += Q^T dA over the rows of subtile RS: product
-    // j is 16-row chunk 2RS + j/(2NDT), head-dim tile (j/2) % NDT, dV (even j)
-    // or dK (odd j)
-    auto p2_load = [&]<int RS>(int j) {
-      return tfrag((j & 1) ? qt : gt, 16 * (2 * RS + j / (2 * NDT)), (j >> 1) % NDT);
-    };
-    auto p2_mma = [&]<int RS>(int j, Frag f) {
-      const int h2 = j / (2 * NDT), dt = (j >> 1) % NDT;
-      if (j & 1) dk[dt] = M::mma(f, bd[RS][h2], dk[dt]);
-      else dv[dt] = M::mma(f, bp[RS][h2], dv[dt]);
-    };
+    // One chain of products per step, one chunk (4 MFMAs) of LDS reads
+    // ahead throughout: S = Q K^T and dP = dO V^T of row subtile 0, then of
+    // subtile 1 (2 NKC products each: chunk j/2, S even, dP odd), then
+    // dV^T += dO^T P and dK^T += Q^T dA over the rows of subtile 0, then of
+    // subtile 1 (4 NDT products each: 16-row chunk 2RS + j/(2NDT), head-dim
+    // tile (j/2) % NDT, dV even, dK odd). Subtile 0's elementwise work runs
+    // beside subtile 1's S/dP products, subtile 1's beside subtile 0's
+    // dK/dV products.
     static_assert(NRS == 2, "two row subtiles per step");
-    // subtile 0's products; subtile 1's products overlap subtile 0's
-    // elementwise work; subtile 0's dK/dV products overlap subtile 1's
-    mfma_phase<2 * NKC, 4, 1>([&](int j) { return p1_load.template operator()<0>(j); },
-                              [&](int j, Frag f) { p1_mma.template operator()<0>(j, f); });
-    mfma_phase_overlap<2 * NKC, 4, 1, 5>([&](int j) { return p1_load.template operator()<1>(j); },
-                                         [&](int j, Frag f) { p1_mma.template operator()<1>(j, f); },
-                                         [&]<int K>() { elem.template operator()<0, K>(); });
-    mfma_phase_overlap<4 * NDT, 4, 2, 5>([&](int j) { return p2_load.template operator()<0>(j); },
-                                         [&](int j, Frag f) { p2_mma.template operator()<0>(j, f); },
-                                         [&]<int K>() { elem.template operator()<1, K>(); });
-    mfma_phase<4 * NDT, 4, 2>([&](int j) { return p2_load.template operator()<1>(j); },
-                              [&](int j, Frag f) { p2_mma.template operator()<1>(j, f); });
+    constexpr int PA = 2 * NKC, PB = 4 * NDT, CA = PA / 4, CB = PB / 4;
+    static_assert(PA % 4 == 0 && PB % 4 == 0, "whole chunks per subtile");
+    auto load = [&]<int J>() -> Frag {
+      if constexpr (J < 2 * PA) {
+        constexpr int rs = J / PA, j = J % PA;
+        return rfrag((j & 1) ? gt : qt, rs, j >> 1);
+      } else {
+        constexpr int rs = (J - 2 * PA) / PB, j = (J - 2 * PA) % PB;
+        return tfrag((j & 1) ? qt : gt, 16 * (2 * rs + j / (2 * NDT)), (j >> 1) % NDT);
+      }
+    };
+    auto mma = [&]<int J>(Frag f) {
+      if constexpr (J < 2 * PA) {
+        constexpr int rs = J / PA, j = J % PA;
+        if constexpr (j & 1) dp[rs] = M::mma(f, vf[j >> 1], dp[rs]);
+        else s[rs] = M::mma(f, kf[j >> 1], s[rs]);
+      } else {
+        constexpr int rs = (J - 2 * PA) / PB, j = (J - 2 * PA) % PB;
+        constexpr int h2 = j / (2 * NDT), dt = (j >> 1) % NDT;
+        if constexpr (j & 1) dk[dt] = M::mma(f, bd[rs][h2], dk[dt]);
+        else dv[dt] = M::mma(f, bp[rs][h2], dv[dt]);
+      }
+    };
+    // slices [lg*5/C, (lg+1)*5/C) of a subtile's elementwise work after
+    // chunk lg of the C chunks it runs beside
+    auto slices = [&]<int RS, int LG, int C>() {
+      [&]<int... K>(std::integer_sequence<int, K...>) {
+        (elem.template operator()<RS, LG * 5 / C + K>(), ...);
+      }(std::make_integer_sequence<int, (LG + 1) * 5 / C - LG * 5 / C>{});
+    };
+    auto after = [&]<int G>() {
+      if constexpr (G >= CA && G < 2 * CA) slices.template operator()<0, G - CA, CA>();
+      else if constexpr (G >= 2 * CA && G < 2 * CA + CB) slices.template operator()<1, G - 2 * CA, CB>();
+    };
+    mfma_chain<2 * CA + 2 * CB, 4>(load, mma, after);
   };
   auto run = [&]<int BUF>(int idx) {
     if (list[idx] & 1) step.template operator()<BUF, true>(idx);

@@ -471,6 +471,36 @@ __device__ __forceinline__ void mfma_phase_overlap(Load&& load, Mfma&& mma, Slic
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// A chain of C chunks of L MFMAs over several products (what would be
+// consecutive phases), with one chunk of read-ahead throughout: the operand
+// reads of chunk g+1 are issued before chunk g's MFMAs, also where the
+// products change, so no phase starts with an exposed LDS latency. Product
+// J is load.template operator()<J>() then mma.template operator()<J>(frag);
+// after.template operator()<g>() (VALU work, which may read results of
+// chunks <= g only) follows chunk g's MFMAs in the same scheduling region.
+template <int C, int L, typename Load, typename Mfma, typename After>
+__device__ __forceinline__ void mfma_chain(Load&& load, Mfma&& mma, After&& after) {
+  typedef decltype(load.template operator()<0>()) F;
+  F buf[2][L];
+  [&]<int... I>(std::integer_sequence<int, I...>) {
+    ((buf[0][I] = load.template operator()<I>()), ...);
+  }(std::make_integer_sequence<int, L>{});
+  [&]<int... G>(std::integer_sequence<int, G...>) {
+    ([&] {
+      constexpr int g = G;
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt untouched
+      __builtin_amdgcn_sched_barrier(0);
+      [&]<int... I>(std::integer_sequence<int, I...>) {
+        if constexpr (g + 1 < C) ((buf[(g + 1) & 1][I] = load.template operator()<(g + 1) * L + I>()), ...);
+        (mma.template operator()<g * L + I>(buf[g & 1][I]), ...);
+      }(std::make_integer_sequence<int, L>{});
+      after.template operator()<g>();
+    }(), ...);
+  }(std::make_integer_sequence<int, C>{});
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // ---------------------------------------------------------------------------
 // 16x16x32 MFMA layout helpers (v_mfma_f32_16x16x32_{bf16,f16}): a C tile
 // of S^T = K Q^T puts query row l%16 in lane l and keys 4*(l/16)+r
