@@ -29,6 +29,8 @@
 // global->LDS copies into swizzled, double-buffered LDS; transposed operands
 // come from ds_read_tr16_b64. Workgroups are numbered head-fastest, so the
 // dispatcher's round-robin over the XCDs keeps one head per XCD L2.
+#include <type_traits>
+
 #include "dense.h"
 #include "report.h"
 #include "tile.h"
@@ -54,6 +56,27 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 }  // namespace
 
+// Table entries per (row, key block). bf16 with blocks of 32+ keys (a wave's
+// 32 keys in one block): 32 bytes, -beta/c2 and eps each as three bf16 terms
+// (zero-padded to 8), which the dK/dV kernel adds to S and dP by one MFMA
+// each (an extra contraction chunk against constant ones), so that no lane
+// reads the table's broadcast values per score. Otherwise the float2
+// (beta, eps).
+template <typename T, int LOGB> struct AugTable {
+  static constexpr bool on = std::is_same<T, bf16>::value && LOGB >= 5;
+  static constexpr int bytes = on ? 32 : 8;
+};
+
+// v as three bf16 terms (v - t0 - t1 - t2 about 2^-24 |v|), zero-padded
+__device__ __forceinline__ bf16x8 split3_bf16(float v) {
+  const bf16 t0 = (bf16)v;
+  const float r0 = v - (float)t0;
+  const bf16 t1 = (bf16)r0;
+  const bf16 t2 = (bf16)(r0 - (float)t1);
+  const bf16 z = (bf16)0.f;
+  return bf16x8{t0, t1, t2, z, z, z, z, z};
+}
+
 DenseBwdPlan dense_bwd_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t H, int64_t D,
                             int64_t block) {
   DenseBwdPlan p = {};
@@ -67,7 +90,8 @@ DenseBwdPlan dense_bwd_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t 
   const int64_t Qp = (Q + kRT - 1) / kRT * kRT;
   const int64_t n_rtiles = Qp / kRT;
   const int64_t nblk = (N + kKT - 1) / kKT * (kKT / block);
-  const size_t tab = sizeof(float2) * (size_t)(B * H) * (size_t)nblk * (size_t)Qp;
+  const size_t ent = dtype == kBF16 && block >= 32 ? 32 : sizeof(float2);  // AugTable<T, LOGB>::bytes
+  const size_t tab = ent * (size_t)(B * H) * (size_t)nblk * (size_t)Qp;
   if (n_rtiles > kMaxRTiles || tab > kMaxTable) return p;
   p.fast = true;
   p.Qp = (int)Qp;
@@ -331,7 +355,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   f32x16 acc[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) acc[dt] = zero16();
+  constexpr bool AUG = AugTable<T, LOGB>::on;
   float2* tab = a.tab + (int64_t)bh * a.nblk * a.Qp;
+  char* taug = reinterpret_cast<char*>(a.tab) + (int64_t)bh * a.nblk * a.Qp * 32;
+  const float inv_c2 = 1.f / a.scale_log2;
   const float c2 = a.scale_log2;
 
   auto step = [&]<int BUF, bool FULL>(int i) {
@@ -401,7 +428,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
           cb[st][j] = fmaf(-mult[st][j], dl, gb[st][j]);
         }
       // table entries of this tile's blocks (one writer per row and block)
-      if (row_in && (BlkSlots<LOGB>::per_half || half == 0)) {
+      if (row_in && (AUG || BlkSlots<LOGB>::per_half || half == 0)) {
         constexpr int STEP = LOGB >= 5 ? ((1 << LOGB) / 32 < NST ? (1 << LOGB) / 32 : NST) : 1;
 #pragma unroll
         for (int st = 0; st < NST; st += STEP)
@@ -424,7 +451,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
               beta = kInf;
               eps = 0.f;
             }
-            tab[(int64_t)bl * a.Qp + row] = make_float2(beta, eps);
+            if constexpr (AUG) {
+              // half 0 the terms of -beta/c2 (+inf: a large finite value),
+              // half 1 those of eps
+              const float nb = fmaxf(fminf(-beta * inv_c2, 1e30f), -1e30f);
+              *reinterpret_cast<bf16x8*>(taug + ((int64_t)bl * a.Qp + row) * 32 + half * 16) =
+                  split3_bf16(half ? eps : nb);
+            } else {
+              tab[(int64_t)bl * a.Qp + row] = make_float2(beta, eps);
+            }
           }
       }
     };
@@ -545,8 +580,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 
   __shared__ __attribute__((aligned(16))) T q1s[QTILE];
   __shared__ __attribute__((aligned(16))) T g0s[QTILE];
   __shared__ __attribute__((aligned(16))) T g1s[QTILE];
-  __shared__ __attribute__((aligned(16))) float2 t0s[NB * MQ];
-  __shared__ __attribute__((aligned(16))) float2 t1s[NB * MQ];
+  constexpr bool AUG = AugTable<T, LOGB>::on;
+  constexpr int TENT = AugTable<T, LOGB>::bytes;
+  __shared__ __attribute__((aligned(16))) char t0s[NB * MQ * TENT];
+  __shared__ __attribute__((aligned(16))) char t1s[NB * MQ * TENT];
   __shared__ __attribute__((aligned(16))) int l0s[MQ];
   __shared__ __attribute__((aligned(16))) int l1s[MQ];
   __shared__ int list[kMaxRTiles];
@@ -689,21 +726,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 
 
   const T* qg = reinterpret_cast<const T*>(a.q) + ((int64_t)bi * a.Q * H + hh) * D;
   const T* gg = reinterpret_cast<const T*>(a.dout) + ((int64_t)bi * a.Q * H + hh) * D;
-  const float2* tg = a.tab + ((int64_t)bh * a.nblk + (int64_t)kt_idx * NB) * a.Qp;
+  const char* tg = reinterpret_cast<const char*>(a.tab) + ((int64_t)bh * a.nblk + (int64_t)kt_idx * NB) * a.Qp * TENT;
   const int* lg = a.lim + (int64_t)bi * a.Qp;
   const Stager<T, DP, WAVES> qst(qg, kstride, a.Q), gst(gg, kstride, a.Q);
   auto stage = [&]<int BUF>(int idx) {
     const int m0 = (list[idx] >> 1) * MQ;
     qst.template stage<MQ>(BUF ? q1s : q0s, m0);
     gst.template stage<MQ>(BUF ? g1s : g0s, m0);
-    // table slice: NB blocks x 64 rows of (beta, eps), 512 contiguous bytes
-    // per block; 16 bytes (two rows) per lane
-    char* tl = reinterpret_cast<char*>(BUF ? t1s : t0s);
+    // table slice: NB blocks x 64 rows, 64 * TENT contiguous bytes per
+    // block, 16 bytes per lane (two float2 rows, or half an entry)
+    char* tl = BUF ? t1s : t0s;
+    constexpr int CPB = MQ * TENT / 16;  // copies per block
 #pragma unroll
-    for (int j0 = 0; j0 < NB * 32; j0 += 256) {
+    for (int j0 = 0; j0 < NB * CPB; j0 += 256) {
       const int j = j0 + (int)threadIdx.x;
-      if (j < NB * 32)
-        async_copy16(tg + (int64_t)(j >> 5) * a.Qp + m0 + 2 * (j & 31), tl + (j0 + 64 * wave) * 16);
+      if (j < NB * CPB)
+        async_copy16(tg + ((int64_t)(j / CPB) * a.Qp + m0) * TENT + (j % CPB) * 16, tl + (j0 + 64 * wave) * 16);
     }
     if (threadIdx.x < 16) async_copy16(lg + m0 + 4 * threadIdx.x, BUF ? l1s : l0s);
   };
@@ -739,8 +777,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 
   f32x16 dk[NDT], dv[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) { dk[dt] = zero16(); dv[dt] = zero16(); }
-  const int tcol = ((32 * wave + col) >> LOGB) * MQ;  // this lane's block in the table slice
+  const int tcol = ((32 * wave + col) >> LOGB) * MQ * TENT;  // this lane's block in the table slice (bytes)
   const float c2 = a.scale_log2;
+  // AugTable: B operands of the table's contraction chunk, ones against the
+  // terms of -beta/c2 (k = 0..2, half 0) for S and of eps (k = 8..10, half 1)
+  // for dP
+  Frag ones_s = {}, ones_dp = {};
+  if constexpr (AUG) {
+    const Frag one3 = {(T)1.f, (T)1.f, (T)1.f, (T)0.f, (T)0.f, (T)0.f, (T)0.f, (T)0.f};
+    ones_s = half ? Frag{} : one3;
+    ones_dp = half ? one3 : Frag{};
+  }
 
   auto step = [&]<int BUF, bool FULL>(int idx) {
     wait_vm();
@@ -748,12 +795,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 
     if (idx + 1 < i1) stage.template operator()<1 - BUF>(idx + 1);
     const T* qt = BUF ? q1s : q0s;
     const T* gt = BUF ? g1s : g0s;
-    const float* tt = reinterpret_cast<const float*>((BUF ? t1s : t0s) + tcol);
+    const char* tb = (BUF ? t1s : t0s) + tcol;
+    const float* tt = reinterpret_cast<const float*>(tb);
     const int* lt = BUF ? l1s : l0s;
 
+    // AugTable: the table's chunk starts S (-beta/c2) and dP (eps)
     f32x16 s[NRS], dp[NRS];
+    if constexpr (!AUG) {
 #pragma unroll
-    for (int rs = 0; rs < NRS; ++rs) { s[rs] = zero16(); dp[rs] = zero16(); }
+      for (int rs = 0; rs < NRS; ++rs) { s[rs] = zero16(); dp[rs] = zero16(); }
+    }
     Frag bp[NRS][2], bd[NRS][2];
     // Elementwise work of row subtile RS, slice I: register group I (rows
     // 32RS + 8I + 4half + 0..3) for I < 4, then the conversion of P and dA
@@ -761,10 +812,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 
     auto elem = [&]<int RS, int I>() {
       if constexpr (I < 4) {
         const int r0 = 32 * RS + 8 * I + 4 * half;
-        const f32x4 t01 = *reinterpret_cast<const f32x4*>(tt + 2 * r0);
-        const f32x4 t23 = *reinterpret_cast<const f32x4*>(tt + 2 * r0 + 4);
-        const float beta[4] = {t01[0], t01[2], t23[0], t23[2]};
-        const float eps[4] = {t01[1], t01[3], t23[1], t23[3]};
+        float beta[4] = {0.f, 0.f, 0.f, 0.f}, eps[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (!AUG) {
+          const f32x4 t01 = *reinterpret_cast<const f32x4*>(tt + 2 * r0);
+          const f32x4 t23 = *reinterpret_cast<const f32x4*>(tt + 2 * r0 + 4);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            beta[j] = t01[2 * j];
+            eps[j] = t01[2 * j + 1];
+            beta[2 + j] = t23[2 * j];
+            eps[2 + j] = t23[2 * j + 1];
+          }
+        }
         int lim[4] = {0, 0, 0, 0};
         if constexpr (!FULL) {
           typedef int i4 __attribute__((ext_vector_type(4)));
@@ -775,8 +834,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int r = 4 * I + j;
-          const float pv = fast_exp2(fmaf(s[RS][r], c2, -beta[j]));
-          const float da = pv * (dp[RS][r] + eps[j]);
+          // AugTable: S and dP already hold -beta/c2 and eps
+          const float pv = AUG ? fast_exp2(s[RS][r] * c2) : fast_exp2(fmaf(s[RS][r], c2, -beta[j]));
+          const float da = AUG ? pv * dp[RS][r] : pv * (dp[RS][r] + eps[j]);
           if constexpr (FULL) {
             s[RS][r] = pv;
             dp[RS][r] = da;
@@ -803,10 +863,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 
     // beside subtile 1's S/dP products, subtile 1's beside subtile 0's
     // dK/dV products.
     static_assert(NRS == 2, "two row subtiles per step");
+    // AugTable: a first chunk of four products starts S and dP of both row
+    // subtiles with the table's terms (row 32RS + col of the lane's block)
+    constexpr int NI = AUG ? 4 : 0, CI = NI / 4;
     constexpr int PA = 2 * NKC, PB = 4 * NDT, CA = PA / 4, CB = PB / 4;
     static_assert(PA % 4 == 0 && PB % 4 == 0, "whole chunks per subtile");
-    auto load = [&]<int J>() -> Frag {
-      if constexpr (J < 2 * PA) {
+    auto load = [&]<int J0>() -> Frag {
+      constexpr int J = J0 - NI;
+      if constexpr (J < 0) {
+        return *reinterpret_cast<const Frag*>(tb + (32 * ((J0 >> 1) & 1) + col) * TENT + half * 16);
+      } else if constexpr (J < 2 * PA) {
         constexpr int rs = J / PA, j = J % PA;
         return rfrag((j & 1) ? gt : qt, rs, j >> 1);
       } else {
@@ -814,8 +880,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 
         return tfrag((j & 1) ? qt : gt, 16 * (2 * rs + j / (2 * NDT)), (j >> 1) % NDT);
       }
     };
-    auto mma = [&]<int J>(Frag f) {
-      if constexpr (J < 2 * PA) {
+    auto mma = [&]<int J0>(Frag f) {
+      constexpr int J = J0 - NI;
+      if constexpr (J < 0) {
+        constexpr int rs = (J0 >> 1) & 1;
+        if constexpr (J0 & 1) dp[rs] = M::mma(f, ones_dp, zero16());
+        else s[rs] = M::mma(f, ones_s, zero16());
+      } else if constexpr (J < 2 * PA) {
         constexpr int rs = J / PA, j = J % PA;
         if constexpr (j & 1) dp[rs] = M::mma(f, vf[j >> 1], dp[rs]);
         else s[rs] = M::mma(f, kf[j >> 1], s[rs]);
@@ -833,11 +904,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 
         (elem.template operator()<RS, LG * 5 / C + K>(), ...);
       }(std::make_integer_sequence<int, (LG + 1) * 5 / C - LG * 5 / C>{});
     };
-    auto after = [&]<int G>() {
+    auto after = [&]<int G0>() {
+      constexpr int G = G0 - CI;
       if constexpr (G >= CA && G < 2 * CA) slices.template operator()<0, G - CA, CA>();
       else if constexpr (G >= 2 * CA && G < 2 * CA + CB) slices.template operator()<1, G - 2 * CA, CB>();
     };
-    mfma_chain<2 * CA + 2 * CB, 4>(load, mma, after);
+    mfma_chain<CI + 2 * CA + 2 * CB, 4>(load, mma, after);
   };
   auto run = [&]<int BUF>(int idx) {
     if (list[idx] & 1) step.template operator()<BUF, true>(idx);
