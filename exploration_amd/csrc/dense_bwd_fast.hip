@@ -57,24 +57,22 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 }  // namespace
 
 // Table entries per (row, key block). bf16 with blocks of 32+ keys (a wave's
-// 32 keys in one block): 32 bytes, -beta/c2 and eps each as three bf16 terms
-// (zero-padded to 8), which the dK/dV kernel adds to S and dP by one MFMA
-// each (an extra contraction chunk against constant ones), so that no lane
-// reads the table's broadcast values per score. Otherwise the float2
+// 32 keys in one block): 16 bytes, -beta/c2 and eps each as three bf16
+// terms (then two zeros), which the dK/dV kernel adds to S and dP by one
+// MFMA each (an extra contraction chunk against constant ones), so that no
+// lane reads the table's broadcast values per score. Otherwise the float2
 // (beta, eps).
 template <typename T, int LOGB> struct AugTable {
   static constexpr bool on = std::is_same<T, bf16>::value && LOGB >= 5;
-  static constexpr int bytes = on ? 32 : 8;
+  static constexpr int bytes = on ? 16 : 8;
 };
 
-// v as three bf16 terms (v - t0 - t1 - t2 about 2^-24 |v|), zero-padded
-__device__ __forceinline__ bf16x8 split3_bf16(float v) {
-  const bf16 t0 = (bf16)v;
-  const float r0 = v - (float)t0;
-  const bf16 t1 = (bf16)r0;
-  const bf16 t2 = (bf16)(r0 - (float)t1);
-  const bf16 z = (bf16)0.f;
-  return bf16x8{t0, t1, t2, z, z, z, z, z};
+// v as three bf16 terms: v - t[0] - t[1] - t[2] is about 2^-24 |v|
+__device__ __forceinline__ void split3_bf16(float v, bf16 (&t)[3]) {
+  t[0] = (bf16)v;
+  const float r0 = v - (float)t[0];
+  t[1] = (bf16)r0;
+  t[2] = (bf16)(r0 - (float)t[1]);
 }
 
 DenseBwdPlan dense_bwd_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t H, int64_t D,
@@ -90,7 +88,7 @@ DenseBwdPlan dense_bwd_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t 
   const int64_t Qp = (Q + kRT - 1) / kRT * kRT;
   const int64_t n_rtiles = Qp / kRT;
   const int64_t nblk = (N + kKT - 1) / kKT * (kKT / block);
-  const size_t ent = dtype == kBF16 && block >= 32 ? 32 : sizeof(float2);  // AugTable<T, LOGB>::bytes
+  const size_t ent = dtype == kBF16 && block >= 32 ? 16 : sizeof(float2);  // AugTable<T, LOGB>::bytes
   const size_t tab = ent * (size_t)(B * H) * (size_t)nblk * (size_t)Qp;
   if (n_rtiles > kMaxRTiles || tab > kMaxTable) return p;
   p.fast = true;
@@ -357,7 +355,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   for (int dt = 0; dt < NDT; ++dt) acc[dt] = zero16();
   constexpr bool AUG = AugTable<T, LOGB>::on;
   float2* tab = a.tab + (int64_t)bh * a.nblk * a.Qp;
-  char* taug = reinterpret_cast<char*>(a.tab) + (int64_t)bh * a.nblk * a.Qp * 32;
+  bf16x8* taug = reinterpret_cast<bf16x8*>(a.tab) + (int64_t)bh * a.nblk * a.Qp;
   const float inv_c2 = 1.f / a.scale_log2;
   const float c2 = a.scale_log2;
 
@@ -428,7 +426,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
           cb[st][j] = fmaf(-mult[st][j], dl, gb[st][j]);
         }
       // table entries of this tile's blocks (one writer per row and block)
-      if (row_in && (AUG || BlkSlots<LOGB>::per_half || half == 0)) {
+      if (row_in && (BlkSlots<LOGB>::per_half || half == 0)) {
         constexpr int STEP = LOGB >= 5 ? ((1 << LOGB) / 32 < NST ? (1 << LOGB) / 32 : NST) : 1;
 #pragma unroll
         for (int st = 0; st < NST; st += STEP)
@@ -452,11 +450,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
               eps = 0.f;
             }
             if constexpr (AUG) {
-              // half 0 the terms of -beta/c2 (+inf: a large finite value),
-              // half 1 those of eps
-              const float nb = fmaxf(fminf(-beta * inv_c2, 1e30f), -1e30f);
-              *reinterpret_cast<bf16x8*>(taug + ((int64_t)bl * a.Qp + row) * 32 + half * 16) =
-                  split3_bf16(half ? eps : nb);
+              // the terms of -beta/c2 (+inf: a large finite value), then of eps
+              bf16 tb_[3], te_[3];
+              split3_bf16(fmaxf(fminf(-beta * inv_c2, 1e30f), -1e30f), tb_);
+              split3_bf16(eps, te_);
+              const bf16 z = (bf16)0.f;
+              taug[(int64_t)bl * a.Qp + row] = bf16x8{tb_[0], tb_[1], tb_[2], te_[0], te_[1], te_[2], z, z};
             } else {
               tab[(int64_t)bl * a.Qp + row] = make_float2(beta, eps);
             }
@@ -734,7 +733,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 
     qst.template stage<MQ>(BUF ? q1s : q0s, m0);
     gst.template stage<MQ>(BUF ? g1s : g0s, m0);
     // table slice: NB blocks x 64 rows, 64 * TENT contiguous bytes per
-    // block, 16 bytes per lane (two float2 rows, or half an entry)
+    // block, 16 bytes per lane (two float2 rows, or one entry)
     char* tl = BUF ? t1s : t0s;
     constexpr int CPB = MQ * TENT / 16;  // copies per block
 #pragma unroll
@@ -779,14 +778,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 
   for (int dt = 0; dt < NDT; ++dt) { dk[dt] = zero16(); dv[dt] = zero16(); }
   const int tcol = ((32 * wave + col) >> LOGB) * MQ * TENT;  // this lane's block in the table slice (bytes)
   const float c2 = a.scale_log2;
-  // AugTable: B operands of the table's contraction chunk, ones against the
-  // terms of -beta/c2 (k = 0..2, half 0) for S and of eps (k = 8..10, half 1)
-  // for dP
+  // AugTable: B operands of the table's contraction chunk (k = 0..7 the
+  // entry, 8..15 zero rows): ones against the terms of -beta/c2 (k = 0..2)
+  // for S and of eps (k = 3..5) for dP
   Frag ones_s = {}, ones_dp = {};
   if constexpr (AUG) {
-    const Frag one3 = {(T)1.f, (T)1.f, (T)1.f, (T)0.f, (T)0.f, (T)0.f, (T)0.f, (T)0.f};
-    ones_s = half ? Frag{} : one3;
-    ones_dp = half ? one3 : Frag{};
+    const T o = (T)1.f, z = (T)0.f;
+    ones_s = half ? Frag{} : Frag{o, o, o, z, z, z, z, z};
+    ones_dp = half ? Frag{} : Frag{z, z, z, o, o, o, z, z};
   }
 
   auto step = [&]<int BUF, bool FULL>(int idx) {
@@ -871,7 +870,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 
     auto load = [&]<int J0>() -> Frag {
       constexpr int J = J0 - NI;
       if constexpr (J < 0) {
-        return *reinterpret_cast<const Frag*>(tb + (32 * ((J0 >> 1) & 1) + col) * TENT + half * 16);
+        return *reinterpret_cast<const Frag*>(tb + (32 * ((J0 >> 1) & 1) + col) * TENT);
       } else if constexpr (J < 2 * PA) {
         constexpr int rs = J / PA, j = J % PA;
         return rfrag((j & 1) ? gt : qt, rs, j >> 1);
