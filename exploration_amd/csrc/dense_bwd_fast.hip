@@ -158,12 +158,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int bi = bh / a.H, hh = bh % a.H;
   const int64_t H = a.H, D = a.D, N = a.N;
 
-  // Key tiles of row tile qt (LDS slot k, one barrier): the count up to the
-  // last visible key of any row, and how many lie below every row's remote
-  // limit (all keys remote, no masks).
-  auto tile_range = [&](int qt, int k, int& n_tiles, int& full) {
+  // Key tiles of row tile qt (LDS slot k): the count up to the last
+  // visible key of any row, and how many lie below every row's remote limit
+  // (all keys remote, no masks). row_pos loads a lane's position,
+  // publish_range writes the wave's part, collect_range (after a barrier)
+  // combines the waves'.
+  auto row_pos = [&](int qt) -> int64_t {
     const int row = qt * 32 * WAVES + wave * 32 + col;
-    const int64_t p = row < a.Q ? a.pos[(int64_t)bi * a.Q + row] : -1;
+    return row < a.Q ? a.pos[(int64_t)bi * a.Q + row] : -1;
+  };
+  auto publish_range = [&](int64_t p, int k) {
     int rl = 0, lh = -1;
     if (p >= 0) {
       const int64_t c = p >> LOGB;
@@ -173,7 +177,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
     const int r0 = wave_max(lh), r1 = wave_min(lh >= 0 ? rl : 0x7fffffff);
     if (lane == 0) { range[k][0][wave] = r0; range[k][1][wave] = r1; }
-    __syncthreads();
+  };
+  auto collect_range = [&](int k, int& n_tiles, int& full) {
     int rg0 = range[k][0][0], rg1 = range[k][1][0];
 #pragma unroll
     for (int w = 1; w < WAVES; ++w) { rg0 = max(rg0, range[k][0][w]); rg1 = min(rg1, range[k][1][w]); }
@@ -194,6 +199,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // split (only where that beats L whole, counting kQPieceCost tiles for the
   // extra piece), an odd middle tile runs whole.
   int qt, piece = 0, n_tiles, full, t0 = 0, t1;
+  int64_t pmine;  // this lane's row position in row tile qt (-1: none)
   bool split = false;
   const int P = n_qtiles / 2, odd = n_qtiles & 1;
   const bool middle = a.q_pair && odd && slot == 2 * P;
@@ -201,8 +207,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int j = slot < P ? slot : (slot < 2 * P ? slot - P : slot - 2 * P - odd);
     const int L = n_qtiles - 1 - j;
     int nL, fL, nS, fS;
-    tile_range(L, 0, nL, fL);
-    tile_range(j, 1, nS, fS);
+    // both row tiles' positions in flight together, one barrier
+    const int64_t pL = row_pos(L), pS = row_pos(j);
+    publish_range(pL, 0);
+    publish_range(pS, 1);
+    __syncthreads();
+    collect_range(0, nL, fL);
+    collect_range(1, nS, fS);
     const int h = min(nL, (nL + nS + kQPieceCost + 1) / 2);
     const bool sp = h > 0 && h < nL && max(h, nL - h + nS + kQPieceCost) < nL;
     if (slot < P) {
@@ -222,10 +233,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
     n_tiles = qt == L ? nL : nS;
     full = qt == L ? fL : fS;
+    pmine = qt == L ? pL : pS;
   } else {
     piece = middle ? 0 : slot / n_qtiles;
     qt = middle ? P : n_qtiles - 1 - slot % n_qtiles;
-    tile_range(qt, 0, n_tiles, full);
+    pmine = row_pos(qt);
+    publish_range(pmine, 0);
+    __syncthreads();
+    collect_range(0, n_tiles, full);
     split = !middle && n_tiles > a.q_split;
     const int h = (n_tiles + a.q_pieces - 1) / a.q_pieces;  // tiles per piece
     t0 = split ? min(piece * h, n_tiles) : 0;
@@ -234,7 +249,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
   const int row = qt * 32 * WAVES + wave * 32 + col;
   const bool row_in = row < a.Q;
-  const int64_t p = row_in ? a.pos[(int64_t)bi * a.Q + row] : -1;
+  const int64_t p = pmine;
 
   // remote keys [0, rlim), local keys [rlim, lhi]; bases of the exponents
   // (+inf for rows without any key, so that every u of theirs is 0)

@@ -101,13 +101,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     return r;
   };
-  // Workgroup key ranges of a row tile (slot k of the LDS table; one barrier):
-  // max remote limit, min / max local key, min remote limit of the rows with
-  // a local window; and from them the tile counts.
+  // Workgroup key ranges of a row tile (slot k of the LDS table): max
+  // remote limit, min / max local key, min remote limit of the rows with a
+  // local window; and from them the tile counts. publish_keys writes a
+  // wave's part, collect_keys (after a barrier) combines the waves'.
   struct TileKeys {
     int n_remote_all, lt0, n_local, full_remote;
   };
-  auto tile_keys = [&](const RowKeys& r, int k) -> TileKeys {
+  auto publish_keys = [&](const RowKeys& r, int k) {
     const bool win = r.lhi >= r.llo;
     const int r0 = wave_max(r.rlim), r1 = wave_min(win ? r.llo : 0x7fffffff);
     const int r2 = wave_max(win ? r.lhi : -1), r3 = wave_min(win ? r.rlim : 0x7fffffff);
@@ -117,7 +118,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       range[k][2][wave] = r2;
       range[k][3][wave] = r3;
     }
-    __syncthreads();
+  };
+  auto collect_keys = [&](int k) -> TileKeys {
     int rg0 = range[k][0][0], rg1 = range[k][1][0], rg2 = range[k][2][0], rg3 = range[k][3][0];
 #pragma unroll
     for (int w = 1; w < WAVES; ++w) {
@@ -144,6 +146,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   bool split = false;  // this job is a piece of a split row tile
   int hsplit = 0;      // remote tiles per piece (the last piece: the rest, and the local tiles)
   TileKeys tk;
+  RowKeys rk;  // this lane's row of row tile qt
   const bool middle = a.f_pair && (n_qtiles & 1) && slot == 2 * (n_qtiles / 2);
   if (a.f_pair && !middle) {
     // pair j: both tiles' key ranges decide whether L is split (the same
@@ -152,7 +155,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int P = n_qtiles / 2, odd = n_qtiles & 1;
     const int j = slot < P ? slot : (slot < 2 * P ? slot - P : slot - 2 * P - odd);
     const int L = n_qtiles - 1 - j;
-    const TileKeys tl = tile_keys(row_keys(L), 0), ts = tile_keys(row_keys(j), 1);
+    // both row tiles' positions in flight together, one barrier
+    const RowKeys rL = row_keys(L), rS = row_keys(j);
+    publish_keys(rL, 0);
+    publish_keys(rS, 1);
+    __syncthreads();
+    const TileKeys tl = collect_keys(0), ts = collect_keys(1);
     const int cL = tl.n_remote_all + tl.n_local, cS = ts.n_remote_all + ts.n_local;
     const int h = min(tl.n_remote_all, (cL + cS + kPieceCost + 1) / 2);
     const bool sp = a.fw0 != nullptr && h > 0 && h < cL && max(h, cL - h + cS + kPieceCost) < cL;
@@ -168,6 +176,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     split = sp && qt == L;
     hsplit = h;
     tk = qt == L ? tl : ts;
+    rk = qt == L ? rL : rS;
   } else {
     // slot mode: slot k takes piece k / n_qtiles of row tile
     // n_qtiles-1-k % n_qtiles (longest causal rows first); an odd middle
@@ -178,7 +187,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       piece = slot / n_qtiles;
       qt = n_qtiles - 1 - slot % n_qtiles;
     }
-    tk = tile_keys(row_keys(qt), 0);
+    rk = row_keys(qt);
+    publish_keys(rk, 0);
+    __syncthreads();
+    tk = collect_keys(0);
     const int n_all = tk.n_remote_all + tk.n_local;
     if (a.fw0 != nullptr && !a.f_pair && n_all > a.f_split) {
       split = true;
@@ -191,7 +203,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const bool last_piece = piece == n_pieces - 1;
   const int row = qt * 128 + wg * 32 + col;
   const bool row_in = row < a.Q;
-  const RowKeys rk = row_keys(qt);
   const int64_t p = rk.p;
   const int rlim = rk.rlim, llo = rk.llo, lhi = rk.lhi;
   // (all of the tile bookkeeping below is workgroup-uniform: kept in SGPRs
