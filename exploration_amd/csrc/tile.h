@@ -407,75 +407,15 @@ __device__ __forceinline__ typename Mma<T>::Frag frag_tr(const T* lds, int k0, i
   return __builtin_bit_cast(typename Mma<T>::Frag, v);
 }
 
-// An MFMA phase of N products whose A operands are read from LDS, run in
-// chunks of L: wait for the reads in flight, issue the reads of chunk g+1,
-// then the L MFMAs of chunk g. The wait is an explicit lgkmcnt(0) at the
-// chunk boundary (with asynchronous global->LDS copies in flight the
-// compiler only ever waits for all LDS reads, so a read issued right before
-// its MFMA would stall it); here every read has a whole chunk of MFMAs to
-// land. load(j) returns the fragment of product j (R LDS reads); mma(j, f)
-// performs it.
-template <int N, int L, int R, typename Load, typename Mfma>
-__device__ __forceinline__ void mfma_phase(Load&& load, Mfma&& mma) {
-  static_assert(N % L == 0, "phase must split into whole chunks");
-  typedef decltype(load(0)) F;
-  F buf[2][L];
-#pragma unroll
-  for (int i = 0; i < L; ++i) buf[0][i] = load(i);
-#pragma unroll
-  for (int g = 0; g < N / L; ++g) {
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt untouched
-    __builtin_amdgcn_sched_barrier(0);
-    if (g + 1 < N / L) {
-#pragma unroll
-      for (int i = 0; i < L; ++i) buf[(g + 1) & 1][i] = load((g + 1) * L + i);
-    }
-#pragma unroll
-    for (int i = 0; i < L; ++i) mma(g * L + i, buf[g & 1][i]);
-    if (g + 1 < N / L) __builtin_amdgcn_sched_group_barrier(0x100, L * R, 0);  // the reads first
-    __builtin_amdgcn_sched_group_barrier(0x008, L, 0);                         // then the MFMAs
-  }
-  __builtin_amdgcn_sched_barrier(0);
-}
-
-// mfma_phase with independent VALU work placed between the chunks: after
-// chunk g's MFMAs, slices [g*NS/C, (g+1)*NS/C) of NS run in the same
-// scheduling region (C = N/L chunks), so one wave overlaps them with its own
-// MFMAs. slice.template operator()<k>() must not read this phase's results.
-template <int N, int L, int R, int NS, typename Load, typename Mfma, typename Slice>
-__device__ __forceinline__ void mfma_phase_overlap(Load&& load, Mfma&& mma, Slice&& slice) {
-  static_assert(N % L == 0, "phase must split into whole chunks");
-  constexpr int C = N / L;
-  typedef decltype(load(0)) F;
-  F buf[2][L];
-#pragma unroll
-  for (int i = 0; i < L; ++i) buf[0][i] = load(i);
-  [&]<int... G>(std::integer_sequence<int, G...>) {
-    ([&] {
-      constexpr int g = G;
-      __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt untouched
-      __builtin_amdgcn_sched_barrier(0);
-      if constexpr (g + 1 < C) {
-#pragma unroll
-        for (int i = 0; i < L; ++i) buf[(g + 1) & 1][i] = load((g + 1) * L + i);
-      }
-#pragma unroll
-      for (int i = 0; i < L; ++i) mma(g * L + i, buf[g & 1][i]);
-      [&]<int... K>(std::integer_sequence<int, K...>) {
-        (slice.template operator()<g * NS / C + K>(), ...);
-      }(std::make_integer_sequence<int, (g + 1) * NS / C - g * NS / C>{});
-    }(), ...);
-  }(std::make_integer_sequence<int, C>{});
-  __builtin_amdgcn_sched_barrier(0);
-}
-
 // A chain of C chunks of L MFMAs over several products (what would be
 // consecutive phases), with one chunk of read-ahead throughout: the operand
 // reads of chunk g+1 are issued before chunk g's MFMAs, also where the
-// products change, so no phase starts with an exposed LDS latency. Product
-// J is load.template operator()<J>() then mma.template operator()<J>(frag);
+// products change, so no phase starts with an exposed LDS latency. The wait
+// is an explicit lgkmcnt(0) at each chunk boundary (with asynchronous
+// global->LDS copies in flight the compiler only ever waits for all LDS
+// reads, so a read issued right before its MFMA would stall it); here every
+// read has a whole chunk of MFMAs to land. Product J is
+// load.template operator()<J>() then mma.template operator()<J>(frag);
 // after.template operator()<g>() (VALU work, which may read results of
 // chunks <= g only) follows chunk g's MFMAs in the same scheduling region.
 template <int C, int L, typename Load, typename Mfma, typename After>
@@ -607,40 +547,11 @@ template <int LOGB> __device__ __forceinline__ bool owns16(int t, int g) {
 
 // An MFMA phase of N products in chunks of L whose A operands are read from
 // LDS (the first NR2 products two reads each, e.g. transposed V fragments,
-// the rest one): wait for the reads in flight, issue the reads of chunk g+1,
-// then the L MFMAs of chunk g (see mfma_phase).
-template <int N, int L, int NR2, typename Load, typename Mfma>
-__device__ __forceinline__ void mfma_chunks(Load&& load, Mfma&& mma) {
-  static_assert(N % L == 0 && NR2 % L == 0, "phase must split into whole chunks");
-  constexpr int C = N / L;
-  typedef decltype(load(0)) F;
-  F buf[2][L];
-#pragma unroll
-  for (int i = 0; i < L; ++i) buf[0][i] = load(i);
-  [&]<int... G>(std::integer_sequence<int, G...>) {
-    ([&] {
-      constexpr int g = G;
-      __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt untouched
-      __builtin_amdgcn_sched_barrier(0);
-      if constexpr (g + 1 < C) {
-#pragma unroll
-        for (int i = 0; i < L; ++i) buf[(g + 1) & 1][i] = load((g + 1) * L + i);
-      }
-#pragma unroll
-      for (int i = 0; i < L; ++i) mma(g * L + i, buf[g & 1][i]);
-      if constexpr (g + 1 < C) __builtin_amdgcn_sched_group_barrier(0x100, L * ((g + 1) * L < NR2 ? 2 : 1), 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, L, 0);
-    }(), ...);
-  }(std::make_integer_sequence<int, C>{});
-  __builtin_amdgcn_sched_barrier(0);
-}
-
-// mfma_chunks where the chunks from NQ0 on also read one fragment shared by
-// their L products (the B operand of the S^T products, one Q fragment per
-// contraction chunk): it is read with the chunk's own operands, one chunk
-// ahead, and handed to mma(j, f, shared) (chunks before NQ0 get an unused
-// fragment).
+// the rest one), read one chunk ahead as in mfma_chain; the chunks from NQ0
+// on also read one fragment shared by their L products (the B operand of
+// the S^T products, one Q fragment per contraction chunk), with the chunk's
+// own operands, and hand it to mma(j, f, shared) (chunks before NQ0 get an
+// unused fragment).
 template <int N, int L, int NR2, int NQ0, typename Load, typename QLoad, typename Mfma>
 __device__ __forceinline__ void mfma_chunks_shared(Load&& load, QLoad&& qload, Mfma&& mma) {
   static_assert(N % L == 0 && NR2 % L == 0 && NQ0 % L == 0, "phase must split into whole chunks");
