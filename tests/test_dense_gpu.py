@@ -220,6 +220,25 @@ def test_cfg2_every_row_at_the_last_position(device):
     _check_dense(q, k, v, pos, do, b, device, torch.bfloat16, oracle_device=device, label="cfg2-last")
 
 
+@pytest.mark.parametrize("d,b", [(64, 32), (128, 64), (128, 128)])
+def test_peaked_scores_bf16(device, d, b):
+    """bf16 with blocks of 32+ keys, where the backward passes the (beta, eps)
+    table to the dK/dV kernel as bf16 terms added by an MFMA: logits with a
+    standard deviation of ~6 (peaked rows, large |beta| and eps), unsorted
+    positions with padding rows and rows past the last key, a partial last
+    key tile and a partial last row tile (oracle in float64 on the CPU)."""
+    print(f"dense peaked d={d} b={b}", flush=True)
+    g = torch.Generator().manual_seed(31 + d + b)
+    n, rows = 520, 140
+    q = (torch.randn(2, rows, 2, d, generator=g) * 2.5).to(torch.bfloat16)
+    k = (torch.randn(2, n, 2, d, generator=g) * 2.5).to(torch.bfloat16)
+    v = torch.randn(2, n, 2, d, generator=g).to(torch.bfloat16)
+    probe = torch.randn(2, rows, 2, d, generator=g).to(torch.bfloat16)
+    pos = torch.randint(-1, n + 20, (2, rows), generator=g)
+    pos[1, :3] = torch.tensor([n - 1, -1, 0])
+    _check_dense(q, k, v, pos, probe, b, device, torch.bfloat16, label=f"peaked d={d} b={b}")
+
+
 @pytest.mark.parametrize("d,b,tiles", [(64, 64, 33), (128, 128, 32), (128, 16, 34)])
 def test_causal_pair_mode(device, d, b, tiles):
     """Causal rows over enough 128-row tiles (B1 H8) that the forward pairs
