@@ -28,7 +28,8 @@ struct DenseArgs {
   int* lim;               // [B,Qp] last visible key of a row, -1 = none
   int* tmin;              // [B,Qp/64] min of lim over 64-row tiles
   int* tmax;              // [B,Qp/64] max of lim over 64-row tiles
-  float2* tab;            // [B*H, nblk, Qp] per (key block, row): (beta, eps)
+  float2* tab;            // [B*H, nblk, Qp] per (key block, row): (beta, eps), or at bf16 with
+                          // blocks of 32+ keys 16 bytes: bf16 terms of -beta/c2 and eps
   // long work items run as pieces whose fp32 partials a merge kernel adds
   // afterwards (each item's first piece writes its flag)
   int* q_count;           // [B*H*n_qtiles] 1 if the dQ item was split

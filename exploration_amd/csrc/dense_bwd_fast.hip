@@ -24,7 +24,9 @@
 //    per row the last visible key, per 64-row tile its min/max (which row
 //    tiles a key tile must visit, and which need masks);
 //  * dense_bwd_dkv_fast: lane = key; per element one exp2 and two FMAs from
-//    the table, no cross-lane or cross-wave reductions, dK/dV in registers.
+//    the table (at bf16 with blocks of 32+ keys the table's terms enter S and
+//    dP through one extra MFMA each, then one multiply each), no cross-lane
+//    or cross-wave reductions, dK/dV in registers.
 // K/V (dQ kernel) and Q/dO (dK/dV kernel) tiles are staged with asynchronous
 // global->LDS copies into swizzled, double-buffered LDS; transposed operands
 // come from ds_read_tr16_b64. Workgroups are numbered head-fastest, so the
@@ -67,7 +69,7 @@ template <typename T, int LOGB> struct AugTable {
   static constexpr int bytes = on ? 16 : 8;
 };
 
-// v as three bf16 terms: v - t[0] - t[1] - t[2] is about 2^-24 |v|
+// v as three bf16 terms: |v - t[0] - t[1] - t[2]| is at most about 2^-26 |v|
 __device__ __forceinline__ void split3_bf16(float v, bf16 (&t)[3]) {
   t[0] = (bf16)v;
   const float r0 = v - (float)t[0];
